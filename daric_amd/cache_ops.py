@@ -1,0 +1,293 @@
+"""`daric.cache_ops` API on the gfx950 HIP library.
+
+Drop-in for the reference's pybind11 module (stub daric/cache_ops.pyi:1-53,
+bindings csrc/cache_ops/bindings.cpp:7-31): `CacheCopier` with
+register_layer / register_store / gather_pages / scatter_pages, and the free
+functions batched_memcpy_d2h / batched_memcpy_h2d keep their signatures,
+argument meaning and errors (RuntimeError with the reference's message text).
+
+Additions (no reference counterpart; the .pyi grows, nothing changes):
+  CacheCopier.register_k_scale, CacheCopier.scatter_pages_rerotate,
+  rerotate_pages, kv_deviation, topk_per_chunk, merge_rows, kernel timing.
+
+Every call is asynchronous on `stream` (0 = the current torch stream of the
+first layer's device, as in reference copier.cpp:27-30). The wrapper keeps
+strong references to registered tensors (copier.cpp:10, 21-24) and records
+temporary inputs on the launch stream (kernels.cu:202, copier.cpp:69).
+"""
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Sequence
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import (DaricChunk, DaricRope, DaricRopeSegment, check, desc, i64_array, load,
+                   str_array)
+
+__all__ = [
+    "CacheCopier", "batched_memcpy_d2h", "batched_memcpy_h2d", "rerotate_pages",
+    "kv_deviation", "topk_per_chunk", "merge_rows", "timing_enable", "timing_read",
+]
+
+
+def _resolve_stream(stream: int, device: Optional[torch.device]) -> int:
+    if stream:
+        return int(stream)
+    if device is None or device.type != "cuda":
+        return 0
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _record(stream: int, device: torch.device, *tensors) -> None:
+    """Keep caching-allocator memory of temporaries alive until `stream` has
+    consumed them (the reference's record_tensor_on_external_stream)."""
+    if device is None or device.type != "cuda":
+        return
+    ext = torch.cuda.ExternalStream(stream, device=device)
+    for t in tensors:
+        if t is not None and t.is_cuda:
+            t.record_stream(ext)
+
+
+def _rope(inv_freq: torch.Tensor, rotary_dim: int, is_neox_style: bool, device) -> DaricRope:
+    if not isinstance(inv_freq, torch.Tensor) or not inv_freq.is_cuda:
+        raise RuntimeError("inv_freq must be a float32 device tensor")
+    if inv_freq.dtype != torch.float32 or not inv_freq.is_contiguous():
+        raise RuntimeError("inv_freq must be a contiguous float32 tensor")
+    if inv_freq.numel() < int(rotary_dim) // 2:
+        raise RuntimeError(f"inv_freq has {inv_freq.numel()} entries, rotary_dim/2 = {int(rotary_dim) // 2}")
+    if device is not None and inv_freq.device != device:
+        raise RuntimeError("inv_freq must be on the KV cache's device")
+    r = DaricRope()
+    r.inv_freq = inv_freq.data_ptr()
+    r.rotary_dim = int(rotary_dim)
+    r.is_neox = 1 if is_neox_style else 0
+    return r
+
+
+class CacheCopier:
+    """Staged KV-cache gather/scatter (reference csrc/cache_ops/copier.cpp)."""
+
+    def __init__(self) -> None:
+        self._lib = load()
+        h = ctypes.c_void_p()
+        check(self._lib.daric_copier_create(ctypes.byref(h)))
+        self._h = h
+        self._layers: dict[str, torch.Tensor] = {}
+        self._scales: dict[str, torch.Tensor] = {}
+        self._store: Optional[torch.Tensor] = None
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.daric_copier_destroy(h)
+            self._h = None
+
+    # -------------------------------------------------------------- register
+    def register_layer(self, name: str, tensor: torch.Tensor, is_page_first: bool) -> None:
+        d = desc(tensor)
+        check(self._lib.daric_copier_register_layer(self._h, str(name).encode(), ctypes.byref(d),
+                                                    1 if is_page_first else 0))
+        self._layers[str(name)] = tensor
+
+    def register_store(self, buffer: torch.Tensor) -> None:
+        d = desc(buffer)
+        check(self._lib.daric_copier_register_store(self._h, ctypes.byref(d)))
+        self._store = buffer
+
+    def register_k_scale(self, name: str, k_scale: Optional[torch.Tensor]) -> None:
+        """Per-head fp32 K scales of an fp8 layer (None clears them)."""
+        d = desc(k_scale) if k_scale is not None else None
+        check(self._lib.daric_copier_register_k_scale(
+            self._h, str(name).encode(), ctypes.byref(d) if d is not None else None))
+        if k_scale is None:
+            self._scales.pop(str(name), None)
+        else:
+            self._scales[str(name)] = k_scale
+
+    # -------------------------------------------------------------- copies
+    def _device(self, layer_names) -> Optional[torch.device]:
+        if len(layer_names) == 0:
+            return None
+        t = self._layers.get(str(layer_names[0]))
+        return t.device if t is not None else None
+
+    def _copy(self, fn, layer_names, offsets, byte_sizes, indices_flat, indices_offsets, stream,
+              extra=()):
+        names = list(layer_names)
+        dev = self._device(names)
+        st = _resolve_stream(stream, dev)
+        idx = desc(indices_flat)
+        status = fn(self._h, str_array(names), len(names), i64_array(offsets), len(offsets),
+                    i64_array(byte_sizes), len(byte_sizes), ctypes.byref(idx),
+                    i64_array(indices_offsets), len(indices_offsets), *extra, ctypes.c_uint64(st))
+        check(status)
+        if names:
+            _record(st, dev, indices_flat)
+
+    def gather_pages(self, layer_names: Sequence[str], offsets: Sequence[int],
+                     byte_sizes: Sequence[int], indices_flat: torch.Tensor,
+                     indices_offsets: Sequence[int], stream: int = 0) -> None:
+        self._copy(self._lib.daric_copier_gather_pages, layer_names, offsets, byte_sizes,
+                   indices_flat, indices_offsets, stream)
+
+    def scatter_pages(self, layer_names: Sequence[str], offsets: Sequence[int],
+                      byte_sizes: Sequence[int], indices_flat: torch.Tensor,
+                      indices_offsets: Sequence[int], stream: int = 0) -> None:
+        self._copy(self._lib.daric_copier_scatter_pages, layer_names, offsets, byte_sizes,
+                   indices_flat, indices_offsets, stream)
+
+    def scatter_pages_rerotate(self, layer_names: Sequence[str], offsets: Sequence[int],
+                               byte_sizes: Sequence[int], indices_flat: torch.Tensor,
+                               indices_offsets: Sequence[int], deltas: Sequence[int],
+                               num_tokens: Sequence[int], inv_freq: torch.Tensor,
+                               rotary_dim: int, is_neox_style: bool = True,
+                               stream: int = 0) -> None:
+        """scatter_pages + re-rotation of the first num_tokens[i] tokens of job
+        i by deltas[i] positions, in one pass (see include/daric_cache_ops.h)."""
+        names = list(layer_names)
+        if len(deltas) != len(names) or len(num_tokens) != len(names):
+            if names:
+                raise RuntimeError("deltas and num_tokens must have one entry per job")
+        dev = self._device(names)
+        rope = _rope(inv_freq, rotary_dim, is_neox_style, dev) if names else DaricRope()
+        self._copy(self._lib.daric_copier_scatter_pages_rerotate, names, offsets, byte_sizes,
+                   indices_flat, indices_offsets, stream,
+                   extra=(i64_array(deltas), i64_array(num_tokens), ctypes.byref(rope)))
+        if names and dev is not None:
+            _record(_resolve_stream(stream, dev), dev, inv_freq)
+
+
+def _memcpy(fn, dev_t, host_t, dev_offsets, host_offsets, sizes, stream, d2h):
+    n = len(sizes)
+    if len(dev_offsets) != n or len(host_offsets) != n:
+        raise RuntimeError("offset and size lists must have the same length")
+    if n == 0:
+        return
+    dev = dev_t.device if dev_t.is_cuda else None
+    st = _resolve_stream(stream, dev)
+    a, b = desc(dev_t), desc(host_t)
+    if d2h:
+        check(fn(ctypes.byref(a), ctypes.byref(b), i64_array(dev_offsets), i64_array(host_offsets),
+                 i64_array(sizes), n, ctypes.c_uint64(st)))
+    else:
+        check(fn(ctypes.byref(b), ctypes.byref(a), i64_array(host_offsets), i64_array(dev_offsets),
+                 i64_array(sizes), n, ctypes.c_uint64(st)))
+
+
+def batched_memcpy_d2h(staging: torch.Tensor, shm: torch.Tensor, stg_offsets: Sequence[int],
+                       shm_offsets: Sequence[int], sizes: Sequence[int], stream: int = 0) -> None:
+    """One hipMemcpyAsync per (stg_offset, shm_offset, size) region (reference
+    helpers.cu:187-217). shm must be page-locked host memory."""
+    _memcpy(load().daric_batched_memcpy_d2h, staging, shm, stg_offsets, shm_offsets, sizes, stream, True)
+
+
+def batched_memcpy_h2d(shm: torch.Tensor, staging: torch.Tensor, shm_offsets: Sequence[int],
+                       stg_offsets: Sequence[int], sizes: Sequence[int], stream: int = 0) -> None:
+    """Mirror of batched_memcpy_d2h (reference helpers.cu:219-248)."""
+    _memcpy(load().daric_batched_memcpy_h2d, staging, shm, stg_offsets, shm_offsets, sizes, stream, False)
+
+
+def _layer_array(layers: Sequence[torch.Tensor]):
+    arr = (_lib.DaricTensor * max(len(layers), 1))()
+    for i, t in enumerate(layers):
+        arr[i] = desc(t)
+    return arr
+
+
+def rerotate_pages(layers: Sequence[torch.Tensor], page_first: bool, block_table: torch.Tensor,
+                   segments: Sequence[tuple[int, int, int, int]], inv_freq: torch.Tensor,
+                   rotary_dim: int, is_neox_style: bool = True,
+                   k_scales: Optional[torch.Tensor] = None, stream: int = 0) -> None:
+    """In-place re-rotation of the K rows of every segment
+    (bt_offset, tok_start, n_tokens, delta) in every layer: the counterpart of
+    the reference's per-layer _launch_triton_rerotate (adapter.py:297-396)."""
+    layers = list(layers)
+    segs = list(segments)
+    if not layers or not segs:
+        return
+    dev = layers[0].device
+    st = _resolve_stream(stream, dev)
+    rope = _rope(inv_freq, rotary_dim, is_neox_style, dev)
+    sarr = (DaricRopeSegment * len(segs))(*[DaricRopeSegment(*(int(x) for x in s)) for s in segs])
+    bt = desc(block_table)
+    ks = desc(k_scales) if k_scales is not None else None
+    check(load().daric_rerotate_pages(_layer_array(layers), len(layers), 1 if page_first else 0,
+                                      ctypes.byref(bt), sarr, len(segs), ctypes.byref(rope),
+                                      ctypes.byref(ks) if ks is not None else None,
+                                      ctypes.c_uint64(st)))
+    _record(st, dev, block_table, inv_freq, k_scales)
+
+
+def _chunks(chunks):
+    ch = list(chunks)
+    return (DaricChunk * max(len(ch), 1))(*[DaricChunk(*(int(x) for x in c)) for c in ch]), len(ch)
+
+
+def kv_deviation(layers: Sequence[torch.Tensor], page_first: bool, block_table: torch.Tensor,
+                 k_new: torch.Tensor, chunks, keys: Optional[torch.Tensor] = None,
+                 stream: int = 0) -> torch.Tensor:
+    """keys[l, row] = sum over (h, d) of (k_new - cached K)^2 in the fixed
+    order of daric_amd/csrc/select_kernels.hip. chunks: (bt_offset,
+    row_offset, n_tokens, k)."""
+    layers = list(layers)
+    dev = layers[0].device
+    if keys is None:
+        keys = torch.zeros(len(layers), k_new.shape[1], dtype=torch.float32, device=dev)
+    st = _resolve_stream(stream, dev)
+    carr, n = _chunks(chunks)
+    bt, kn, kd = desc(block_table), desc(k_new), desc(keys)
+    check(load().daric_kv_deviation(_layer_array(layers), len(layers), 1 if page_first else 0,
+                                    ctypes.byref(bt), ctypes.byref(kn), carr, n, ctypes.byref(kd),
+                                    ctypes.c_uint64(st)))
+    _record(st, dev, block_table, k_new, keys)
+    return keys
+
+
+def topk_per_chunk(keys: torch.Tensor, chunks, kmax: Optional[int] = None,
+                   out: Optional[torch.Tensor] = None, stream: int = 0) -> torch.Tensor:
+    """Per (layer, chunk) the k largest keys, ties to the lower index; chunk-
+    local indices ascending, padded with -1 to kmax."""
+    ch = list(chunks)
+    if kmax is None:
+        kmax = max([min(int(c[3]), int(c[2])) for c in ch] + [0])
+    if out is None:
+        out = torch.empty(keys.shape[0], len(ch), kmax, dtype=torch.int32, device=keys.device)
+    st = _resolve_stream(stream, keys.device)
+    carr, n = _chunks(ch)
+    kd, od = desc(keys), desc(out)
+    check(load().daric_topk_per_chunk(ctypes.byref(kd), carr, n, ctypes.byref(od), ctypes.c_uint64(st)))
+    _record(st, keys.device, keys, out)
+    return out
+
+
+def merge_rows(layers: Sequence[torch.Tensor], page_first: bool, block_table: torch.Tensor,
+               k_new: torch.Tensor, v_new: Optional[torch.Tensor], chunks, sel_idx: torch.Tensor,
+               stream: int = 0) -> None:
+    """Write the selected recomputed K/V rows into their paged-cache slots."""
+    layers = list(layers)
+    dev = layers[0].device
+    st = _resolve_stream(stream, dev)
+    carr, n = _chunks(chunks)
+    bt, kn, si = desc(block_table), desc(k_new), desc(sel_idx)
+    vn = desc(v_new) if v_new is not None else None
+    check(load().daric_merge_rows(_layer_array(layers), len(layers), 1 if page_first else 0,
+                                  ctypes.byref(bt), ctypes.byref(kn),
+                                  ctypes.byref(vn) if vn is not None else None, carr, n,
+                                  ctypes.byref(si), ctypes.c_uint64(st)))
+    _record(st, dev, block_table, k_new, v_new, sel_idx)
+
+
+def timing_enable(enable: bool = True) -> None:
+    check(load().daric_timing_enable(1 if enable else 0))
+
+
+def timing_read() -> tuple[float, int]:
+    """(summed kernel milliseconds, launches) since the last read."""
+    ms = ctypes.c_double()
+    n = ctypes.c_int64()
+    check(load().daric_timing_read(ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value

@@ -1,0 +1,889 @@
+// C ABI of the KV-reuse hot path: CacheCopier, batched copies, re-rotation,
+// recompute selection. Host-side validation follows the reference's checks
+// (csrc/cache_ops/helpers.cu:15-174, copier.cpp:7-111, kernels.cu:127-330)
+// in the same order and with the same messages; no device work is enqueued
+// before every check has passed.
+#include <algorithm>
+#include <limits>
+#include <map>
+#include <string>
+#include <tuple>
+#include <unordered_map>
+
+#include "common.h"
+#include "elem.h"
+#include "kernels.h"
+
+using namespace daric;
+
+namespace {
+
+constexpr int64_t kInt64Max = std::numeric_limits<int64_t>::max();
+constexpr int64_t kIntMax = std::numeric_limits<int>::max();
+constexpr int64_t kMaxTiles = (1ll << 24) - 1;  // grid.x * 256 lanes must stay < 2^32
+
+int64_t checked_multiply(int64_t lhs, int64_t rhs, const char* context) {
+    DARIC_CHECK(lhs >= 0 && rhs >= 0, context, " must be non-negative");
+    DARIC_CHECK(lhs == 0 || rhs <= kInt64Max / lhs, context, " exceeds int64 range");
+    return lhs * rhs;
+}
+
+// helpers.cu:22-64
+int64_t dense_span_elements(const daric_tensor& t, int first_dim) {
+    struct Dim { int dim; int64_t size, stride; };
+    std::vector<Dim> dims;
+    for (int d = first_dim; d < t.ndim; ++d) {
+        const int64_t size = t.sizes[d], stride = t.strides[d];
+        DARIC_CHECK(size > 0, "KV cache copy dimensions must be non-empty", " | shape=", sizes_str(t),
+                    " | stride=", strides_str(t), " | failed_dim=", d);
+        if (size == 1) continue;
+        DARIC_CHECK(stride > 0, "KV cache non-singleton dimensions must have positive strides",
+                    " | shape=", sizes_str(t), " | stride=", strides_str(t), " | failed_dim=", d,
+                    " | actual_stride=", stride);
+        dims.push_back({d, size, stride});
+    }
+    std::sort(dims.begin(), dims.end(), [](const Dim& a, const Dim& b) { return a.stride < b.stride; });
+    int64_t expected = 1;
+    for (const auto& dm : dims) {
+        DARIC_CHECK(dm.stride == expected, "KV cache copy dimensions must form a dense physical span",
+                    " | shape=", sizes_str(t), " | stride=", strides_str(t), " | failed_dim=", dm.dim,
+                    " | expected_stride=", expected, " | actual_stride=", dm.stride,
+                    " | relation=", dm.stride > expected ? "hole" : "overlap");
+        expected = checked_multiply(expected, dm.size, "KV cache dense span");
+    }
+    return expected;
+}
+
+// helpers.cu:66-90
+void validate_outer_regions(const daric_tensor& t, int64_t prefix_size, int64_t num_pages,
+                            int64_t prefix_stride, int64_t page_stride, int64_t suffix) {
+    std::vector<std::pair<int64_t, int64_t>> axes;
+    if (prefix_size > 1) axes.emplace_back(prefix_stride, prefix_size);
+    if (num_pages > 1) axes.emplace_back(page_stride, num_pages);
+    std::sort(axes.begin(), axes.end());
+    int64_t occupied = suffix;
+    for (const auto& [stride, size] : axes) {
+        DARIC_CHECK(stride >= occupied, "KV cache prefix/page regions overlap", " | shape=",
+                    sizes_str(t), " | stride=", strides_str(t), " | region_size=", suffix,
+                    " | required_stride=", occupied, " | actual_stride=", stride);
+        const int64_t extent = checked_multiply(size - 1, stride, "KV cache outer span");
+        DARIC_CHECK(extent <= kInt64Max - occupied, "KV cache outer span exceeds int64 range");
+        occupied += extent;
+    }
+}
+
+struct PageShape {
+    int64_t num_pages, prefix_size, page_stride, suffix, prefix_stride;
+};
+
+// helpers.cu:94-148
+PageShape page_copy_shape(const daric_tensor& t, bool page_first) {
+    DARIC_CHECK(t.device >= 0, "KV cache tensor must be on CUDA");
+    DARIC_CHECK(t.ndim >= 1, "KV cache tensor must have at least one dimension");
+    const int64_t e = t.elem_size;
+    PageShape s{};
+    if (page_first) {
+        DARIC_CHECK(t.sizes[0] > 0, "page dimension must be non-zero");
+        DARIC_CHECK(t.sizes[0] <= kIntMax, "number of pages exceeds int range: ", t.sizes[0]);
+        s.num_pages = t.sizes[0];
+        s.prefix_size = 1;
+        s.prefix_stride = 0;
+        s.page_stride = checked_multiply(t.strides[0], e, "KV cache page stride");
+        s.suffix = checked_multiply(dense_span_elements(t, 1), e, "KV cache page span");
+        if (s.num_pages > 1)
+            DARIC_CHECK(s.page_stride >= s.suffix, "KV cache pages overlap", " | shape=", sizes_str(t),
+                        " | stride=", strides_str(t), " | page_stride=", s.page_stride,
+                        " | page_span=", s.suffix);
+    } else {
+        DARIC_CHECK(t.ndim >= 2, "non-page-first KV cache tensor must have at least two dimensions");
+        DARIC_CHECK(t.sizes[0] > 0, "prefix dimension must be non-zero");
+        DARIC_CHECK(t.sizes[1] > 0, "page dimension must be non-zero");
+        DARIC_CHECK(t.sizes[0] <= kIntMax, "prefix size exceeds int range: ", t.sizes[0]);
+        DARIC_CHECK(t.sizes[1] <= kIntMax, "number of pages exceeds int range: ", t.sizes[1]);
+        s.prefix_size = t.sizes[0];
+        s.num_pages = t.sizes[1];
+        s.prefix_stride = checked_multiply(t.strides[0], e, "KV cache prefix stride");
+        s.page_stride = checked_multiply(t.strides[1], e, "KV cache page stride");
+        s.suffix = checked_multiply(dense_span_elements(t, 2), e, "KV cache suffix span");
+        validate_outer_regions(t, s.prefix_size, s.num_pages, s.prefix_stride, s.page_stride, s.suffix);
+    }
+    DARIC_CHECK(s.page_stride > 0, "page_stride must be positive");
+    return s;
+}
+
+// helpers.cu:150-174
+void validate_common_job_inputs(int64_t n_jobs, const int64_t* offsets, int64_t n_offsets,
+                                const int64_t* byte_sizes, int64_t n_byte_sizes,
+                                const int64_t* indices_offsets, int64_t n_indices_offsets,
+                                const daric_tensor* indices) {
+    DARIC_CHECK(n_offsets == n_jobs && offsets != nullptr, "offsets length mismatch");
+    DARIC_CHECK(n_byte_sizes == n_jobs && byte_sizes != nullptr, "byte_sizes length mismatch");
+    DARIC_CHECK(n_indices_offsets == n_jobs + 1 && indices_offsets != nullptr,
+                "indices_offsets size must be num_jobs + 1");
+    check_tensor_struct(indices, "indices_flat");
+    DARIC_CHECK(indices->device >= 0, "indices_flat must be on CUDA");
+    DARIC_CHECK(indices->ndim == 1, "indices_flat must be 1D");
+    DARIC_CHECK(indices->dtype == DARIC_DTYPE_INT32, "indices_flat must be int32");
+    DARIC_CHECK(is_contiguous(*indices), "indices_flat must be contiguous");
+    DARIC_CHECK(indices_offsets[0] >= 0, "indices_offsets[0] must be non-negative");
+    DARIC_CHECK(indices_offsets[n_jobs] <= numel(*indices),
+                "indices_offsets.back() exceeds indices_flat.numel()");
+    for (int64_t i = 0; i < n_jobs; ++i) {
+        DARIC_CHECK(offsets[i] >= 0, "negative store offset at job ", i);
+        DARIC_CHECK(byte_sizes[i] >= 0, "negative byte size at job ", i);
+        DARIC_CHECK(indices_offsets[i] >= 0, "negative indices offset at job ", i);
+        DARIC_CHECK(indices_offsets[i] <= indices_offsets[i + 1],
+                    "indices_offsets must be non-decreasing at job ", i);
+    }
+}
+
+int elem_kind(const daric_tensor& t) {
+    switch (t.dtype) {
+        case DARIC_DTYPE_BFLOAT16: return kBF16;
+        case DARIC_DTYPE_FLOAT16: return kF16;
+        case DARIC_DTYPE_UINT8:
+        case DARIC_DTYPE_FP8_E4M3FN: return kE4M3;
+        default: return -1;
+    }
+}
+
+// Rotary layout resolution of reference adapter.py:311-368.
+struct RopeLayout {
+    int64_t PS, H, D, sb, ss, sh, num_blocks, row_width;
+};
+
+RopeLayout rope_layout(const daric_tensor& t, bool page_first, int rotary_dim) {
+    RopeLayout r{};
+    if (t.ndim == 5) {
+        r.PS = t.sizes[2]; r.H = t.sizes[3]; r.D = t.sizes[4];
+        if (page_first) { r.sb = t.strides[0]; r.num_blocks = t.sizes[0]; }
+        else { r.sb = t.strides[1]; r.num_blocks = t.sizes[1]; }
+        r.ss = t.strides[2]; r.sh = t.strides[3];
+        r.row_width = r.D;
+        DARIC_CHECK(t.strides[4] == 1 || r.D == 1, "KV cache head_dim stride must equal 1 for rerotate");
+    } else if (t.ndim == 4) {
+        const char* constraint = nullptr;
+        if (!page_first) constraint = "page_first must be true";
+        else if (t.sizes[3] <= 0 || t.sizes[3] % 2 != 0) constraint = "packed content dimension must be positive and even";
+        else if (t.strides[3] != 1) constraint = "packed content feature stride must equal 1";
+        const int64_t hd = t.sizes[3] / 2;
+        if (!constraint && (rotary_dim <= 0 || rotary_dim % 2 != 0 || rotary_dim > hd))
+            constraint = "rotary_dim must be positive, even, and no greater than the packed K head dimension";
+        if (constraint)
+            throw Error(DARIC_ERR_INVALID,
+                        cat("Invalid 4D KV cache for rerotate: shape=", sizes_str(t), ", stride=",
+                            strides_str(t), ", rotary_dim=", rotary_dim, ", constraint=", constraint));
+        r.PS = t.sizes[2]; r.H = t.sizes[1]; r.D = hd;
+        r.sb = t.strides[0]; r.ss = t.strides[2]; r.sh = t.strides[1];
+        r.num_blocks = t.sizes[0];
+        r.row_width = 2 * hd;
+    } else if (t.ndim == 3) {
+        r.PS = t.sizes[1]; r.H = 1; r.D = t.sizes[2];
+        r.sb = t.strides[0]; r.ss = t.strides[1]; r.sh = 0;
+        r.num_blocks = t.sizes[0];
+        r.row_width = r.D;
+        DARIC_CHECK(t.strides[2] == 1 || r.D == 1, "KV cache hidden stride must equal 1 for rerotate");
+    } else {
+        throw Error(DARIC_ERR_INVALID, cat("Unsupported KV cache rank for rerotate: ", t.ndim));
+    }
+    DARIC_CHECK(rotary_dim > 0 && rotary_dim % 2 == 0 && rotary_dim <= r.D,
+                "rotary_dim must be positive, even and no greater than head_dim (", r.D,
+                "), got ", rotary_dim);
+    DARIC_CHECK(r.num_blocks <= kIntMax && r.PS <= kIntMax && r.H <= kIntMax,
+                "KV cache dimensions exceed int range");
+    return r;
+}
+
+void check_rope(const daric_rope* rope) {
+    DARIC_CHECK(rope != nullptr, "rope parameters must not be null");
+    DARIC_CHECK(rope->inv_freq != nullptr, "inv_freq must not be null");
+    DARIC_CHECK(rope->rotary_dim > 0 && rope->rotary_dim % 2 == 0 && rope->rotary_dim / 2 <= 256,
+                "rotary_dim must be positive, even and at most 512, got ", rope->rotary_dim);
+}
+
+bool aligned(const void* p, int64_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+hipStream_t as_stream(uint64_t s) { return reinterpret_cast<hipStream_t>(static_cast<uintptr_t>(s)); }
+
+}  // namespace
+
+// ====================================================================== copier
+struct daric_copier {
+    struct Layer {
+        daric_tensor t;
+        bool page_first;
+        const float* k_scale = nullptr;
+        int64_t k_scale_numel = 0;
+    };
+    std::unordered_map<std::string, Layer> layers;
+    daric_tensor store{};
+    bool has_store = false;
+    std::mutex mu;  // registration vs. lookups from concurrent calls
+};
+
+namespace {
+
+struct ResolvedJobs {
+    std::vector<CopyJob> jobs;
+    std::vector<const daric_copier::Layer*> layers;
+    int64_t max_tiles = 0;
+    int64_t max_elements = 0;
+    int vw = 16;
+    int device = -1;
+};
+
+// Shared front half of gather/scatter: the reference's check order
+// (copier.cpp:46-66) followed by the launcher's per-job shape and byte-size
+// checks (kernels.cu:135-161).
+ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_jobs,
+                          const int64_t* offsets, int64_t n_offsets, const int64_t* byte_sizes,
+                          int64_t n_byte_sizes, const daric_tensor* indices,
+                          const int64_t* indices_offsets, int64_t n_indices_offsets, bool gather) {
+    ResolvedJobs r;
+    DARIC_CHECK(c->has_store, "store buffer not registered; call register_store() first");
+    if (n_jobs == 0) return r;
+    DARIC_CHECK(n_jobs > 0 && names != nullptr, "layer_names must not be empty");
+    validate_common_job_inputs(n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices_offsets,
+                               n_indices_offsets, indices);
+    const int64_t store_size = numel(c->store);
+    for (int64_t i = 0; i < n_jobs; ++i) {
+        DARIC_CHECK(offsets[i] >= 0, "negative store offset at job ", i);
+        DARIC_CHECK(byte_sizes[i] >= 0, "negative store byte size at job ", i);
+        DARIC_CHECK(offsets[i] <= store_size, "store offset out of range at job ", i);
+        DARIC_CHECK(byte_sizes[i] <= store_size - offsets[i], "store range out of bounds at job ", i);
+    }
+    r.layers.reserve(n_jobs);
+    for (int64_t i = 0; i < n_jobs; ++i) {
+        DARIC_CHECK(names[i] != nullptr, "layer not registered: (null)");
+        auto it = c->layers.find(names[i]);
+        DARIC_CHECK(it != c->layers.end(), "layer not registered: ", names[i]);
+        r.layers.push_back(&it->second);
+    }
+    r.device = r.layers[0]->t.device;
+    DARIC_CHECK(indices->device == r.device, "indices_flat must be on the same device as kvcache");
+    for (int64_t i = 0; i < n_jobs; ++i) {
+        DARIC_CHECK(r.layers[i]->t.device >= 0, gather ? "all source layers must be CUDA tensors; job "
+                                                       : "all destination layers must be CUDA tensors; job ", i);
+        DARIC_CHECK(r.layers[i]->t.device == r.device,
+                    gather ? "all source layers must be on the same device; job "
+                           : "all destination layers must be on the same device; job ", i);
+    }
+    uint8_t* store = static_cast<uint8_t*>(c->store.data);
+    const int32_t* idx = static_cast<const int32_t*>(indices->data);
+    r.jobs.resize(n_jobs);
+    bool a16 = aligned(store, 16), a4 = aligned(store, 4);
+    for (int64_t i = 0; i < n_jobs; ++i) {
+        const daric_tensor& t = r.layers[i]->t;
+        const PageShape s = page_copy_shape(t, r.layers[i]->page_first);
+        const int64_t n_sel = indices_offsets[i + 1] - indices_offsets[i];
+        const int64_t num = s.prefix_size * n_sel * s.suffix;
+        if (byte_sizes[i] != num)
+            throw Error(DARIC_ERR_RUNTIME,
+                        cat("byte_size mismatch at job ", i, " | C++ expected bytes: ", num,
+                            " | Python passed bytes: ", byte_sizes[i], " | Tensor shape: ",
+                            sizes_str(t), " | Tensor strides: ", strides_str(t)));
+        DARIC_CHECK(n_sel <= kIntMax, "too many selected pages at job ", i);
+        DARIC_CHECK(s.suffix <= kIntMax, "page span exceeds int range at job ", i);
+        CopyJob& j = r.jobs[i];
+        j.layer = static_cast<uint8_t*>(t.data);
+        j.stage = store + offsets[i];
+        j.idx = idx + indices_offsets[i];
+        j.k_scale = r.layers[i]->k_scale;
+        j.prefix_stride = s.prefix_stride;
+        j.page_stride = s.page_stride;
+        j.span = s.suffix;
+        j.n_sel = static_cast<int32_t>(n_sel);
+        j.prefix = static_cast<int32_t>(s.prefix_size);
+        j.num_pages = static_cast<int32_t>(s.num_pages);
+        j.n_tokens = 0;
+        j.delta = 0.0f;
+        r.max_tiles = std::max(r.max_tiles, s.prefix_size * n_sel);
+        r.max_elements = std::max(r.max_elements, num);
+        const auto al = [&](int64_t a) {
+            return s.suffix % a == 0 && s.page_stride % a == 0 && s.prefix_stride % a == 0 &&
+                   offsets[i] % a == 0 && aligned(t.data, a);
+        };
+        a16 = a16 && al(16);
+        a4 = a4 && al(4);
+    }
+    DARIC_CHECK(r.max_tiles <= kMaxTiles, "too many pages in one job: ", r.max_tiles);
+    r.vw = a16 ? 16 : (a4 ? 4 : 1);
+    return r;
+}
+
+int copy_pages(daric_copier* c, const char* const* names, int64_t n_jobs, const int64_t* offsets,
+               int64_t n_offsets, const int64_t* byte_sizes, int64_t n_byte_sizes,
+               const daric_tensor* indices, const int64_t* indices_offsets,
+               int64_t n_indices_offsets, uint64_t stream, bool gather) {
+    return guarded([&] {
+        DARIC_CHECK(c != nullptr, "copier must not be null");
+        std::lock_guard<std::mutex> lk(c->mu);
+        ResolvedJobs r = resolve_jobs(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes,
+                                      indices, indices_offsets, n_indices_offsets, gather);
+        if (r.jobs.empty() || r.max_elements == 0) return;
+        DeviceGuard guard(r.device);
+        const hipStream_t st = as_stream(stream);
+        DescUpload up(r.device, r.jobs.data(), r.jobs.size() * sizeof(CopyJob), st);
+        LaunchTimer timer(st);
+        launch_copy_pages(static_cast<const CopyJob*>(up.get()), static_cast<int>(r.jobs.size()),
+                          static_cast<int>(r.max_tiles), r.vw, gather, st);
+    });
+}
+
+// Row model of a page span for the fused kernel; returns false when the
+// layout does not have dense K head rows (the fused path then refuses).
+bool row_geometry(const daric_tensor& t, bool page_first, const RopeLayout& L, int rotary_dim,
+                  bool neox, int64_t span_bytes, RowGeom* out, std::string* why) {
+    const int64_t e = t.elem_size;
+    const int64_t W = L.row_width;
+    const int kind = elem_kind(t);
+    const int64_t VE = kind == kE4M3 ? 16 : 8;
+    int64_t tok_div;
+    if (L.H == 1 || L.PS == 1) {
+        tok_div = L.H == 1 ? 1 : L.H;
+        if (L.H == 1 && L.PS > 1 && L.ss != W) { *why = "token rows are not dense"; return false; }
+        if (L.PS == 1 && L.H > 1 && L.sh != W) { *why = "head rows are not dense"; return false; }
+    } else if (L.ss == L.H * W && L.sh == W) {
+        tok_div = L.H;  // [.., PS, H, D]
+    } else if (L.sh == L.PS * W && L.ss == W) {
+        tok_div = 1;    // [.., H, PS, D]
+    } else {
+        *why = "K head rows are not dense in the page span";
+        return false;
+    }
+    const int64_t krows = L.PS * L.H;
+    int64_t n_rows = krows;
+    if (t.ndim == 5 && page_first) {
+        if (t.strides[1] != krows * W) { *why = "the V half does not follow the K half in a page"; return false; }
+        n_rows = 2 * krows;
+    }
+    if (n_rows * W * e != span_bytes) { *why = "page span is not the K/V head rows"; return false; }
+    if ((W * e) % 16 != 0) { *why = "row bytes are not a multiple of 16"; return false; }
+    const int64_t rot_units_elems = neox ? rotary_dim / 2 : rotary_dim;
+    if (rot_units_elems % VE != 0) { *why = "rotary pairs are not 16-byte aligned"; return false; }
+    RowGeom g{};
+    g.W = static_cast<int32_t>(W);
+    g.n_rows = static_cast<int32_t>(n_rows);
+    g.krows = static_cast<int32_t>(krows);
+    g.tok_div = static_cast<int32_t>(tok_div);
+    g.PS = static_cast<int32_t>(L.PS);
+    g.H = static_cast<int32_t>(L.H);
+    g.R = rotary_dim;
+    g.n_rot = static_cast<int32_t>(rot_units_elems / VE);
+    g.ipr = static_cast<int32_t>(g.n_rot + (W - rotary_dim) / VE);
+    *out = g;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int daric_copier_create(daric_copier** out) {
+    return guarded([&] {
+        DARIC_CHECK(out != nullptr, "out must not be null");
+        *out = new daric_copier();
+    });
+}
+
+int daric_copier_destroy(daric_copier* copier) {
+    return guarded([&] { delete copier; });
+}
+
+int daric_copier_register_layer(daric_copier* c, const char* name, const daric_tensor* tensor,
+                                int is_page_first) {
+    return guarded([&] {
+        DARIC_CHECK(c != nullptr && name != nullptr, "copier and name must not be null");
+        check_tensor_struct(tensor, "kvcache tensor");
+        DARIC_CHECK(tensor->device >= 0, "kvcache tensor must be on GPU: ", name);
+        std::lock_guard<std::mutex> lk(c->mu);
+        daric_copier::Layer L{*tensor, is_page_first != 0, nullptr, 0};
+        auto it = c->layers.find(name);
+        if (it != c->layers.end()) {
+            L.k_scale = it->second.k_scale;
+            L.k_scale_numel = it->second.k_scale_numel;
+        }
+        c->layers.insert_or_assign(name, L);
+    });
+}
+
+int daric_copier_register_store(daric_copier* c, const daric_tensor* buffer) {
+    return guarded([&] {
+        DARIC_CHECK(c != nullptr, "copier must not be null");
+        check_tensor_struct(buffer, "store buffer");
+        DARIC_CHECK(buffer->device >= 0, "staging buffer must be on CUDA");
+        DARIC_CHECK(buffer->ndim == 1, "store buffer must be 1D");
+        DARIC_CHECK(buffer->dtype == DARIC_DTYPE_UINT8, "store buffer must be uint8");
+        DARIC_CHECK(is_contiguous(*buffer), "store buffer must be contiguous");
+        std::lock_guard<std::mutex> lk(c->mu);
+        c->store = *buffer;
+        c->has_store = true;
+    });
+}
+
+int daric_copier_register_k_scale(daric_copier* c, const char* name, const daric_tensor* k_scale) {
+    return guarded([&] {
+        DARIC_CHECK(c != nullptr && name != nullptr, "copier and name must not be null");
+        std::lock_guard<std::mutex> lk(c->mu);
+        auto it = c->layers.find(name);
+        DARIC_CHECK(it != c->layers.end(), "layer not registered: ", name);
+        if (k_scale == nullptr || k_scale->data == nullptr) {
+            it->second.k_scale = nullptr;
+            it->second.k_scale_numel = 0;
+            return;
+        }
+        DARIC_CHECK(k_scale->device == it->second.t.device, "k_scale must be on the layer's device");
+        DARIC_CHECK(k_scale->dtype == DARIC_DTYPE_FLOAT32 && is_contiguous(*k_scale),
+                    "k_scale must be a contiguous float32 tensor");
+        it->second.k_scale = static_cast<const float*>(k_scale->data);
+        it->second.k_scale_numel = numel(*k_scale);
+    });
+}
+
+int daric_copier_gather_pages(daric_copier* c, const char* const* names, int64_t n_jobs,
+                              const int64_t* offsets, int64_t n_offsets, const int64_t* byte_sizes,
+                              int64_t n_byte_sizes, const daric_tensor* indices,
+                              const int64_t* indices_offsets, int64_t n_indices_offsets,
+                              uint64_t stream) {
+    return copy_pages(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices,
+                      indices_offsets, n_indices_offsets, stream, true);
+}
+
+int daric_copier_scatter_pages(daric_copier* c, const char* const* names, int64_t n_jobs,
+                              const int64_t* offsets, int64_t n_offsets, const int64_t* byte_sizes,
+                              int64_t n_byte_sizes, const daric_tensor* indices,
+                              const int64_t* indices_offsets, int64_t n_indices_offsets,
+                              uint64_t stream) {
+    return copy_pages(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices,
+                      indices_offsets, n_indices_offsets, stream, false);
+}
+
+int daric_copier_scatter_pages_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs,
+                                        const int64_t* offsets, int64_t n_offsets,
+                                        const int64_t* byte_sizes, int64_t n_byte_sizes,
+                                        const daric_tensor* indices,
+                                        const int64_t* indices_offsets, int64_t n_indices_offsets,
+                                        const int64_t* deltas, const int64_t* num_tokens,
+                                        const daric_rope* rope, uint64_t stream) {
+    return guarded([&] {
+        DARIC_CHECK(c != nullptr, "copier must not be null");
+        std::lock_guard<std::mutex> lk(c->mu);
+        ResolvedJobs r = resolve_jobs(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes,
+                                      indices, indices_offsets, n_indices_offsets, false);
+        if (r.jobs.empty() || r.max_elements == 0) return;
+        check_rope(rope);
+        DARIC_CHECK(deltas != nullptr && num_tokens != nullptr, "deltas and num_tokens must not be null");
+        DARIC_CHECK(r.vw == 16, "fused scatter+rerotate needs 16-byte aligned pages, strides and offsets");
+        // Group jobs by row geometry and element type; one launch per group.
+        using Key = std::tuple<int, int, int, int, int, int, int, int, int>;
+        std::map<Key, std::vector<int64_t>> groups;
+        std::map<Key, RowGeom> geoms;
+        for (int64_t i = 0; i < n_jobs; ++i) {
+            const auto* L = r.layers[i];
+            const int kind = elem_kind(L->t);
+            DARIC_CHECK(kind >= 0, "unsupported KV cache dtype for rerotate at job ", i);
+            DARIC_CHECK(deltas[i] > -(1ll << 24) && deltas[i] < (1ll << 24),
+                        "delta out of range at job ", i, ": ", deltas[i]);
+            DARIC_CHECK(num_tokens[i] >= 0, "negative num_tokens at job ", i);
+            const RopeLayout lay = rope_layout(L->t, L->page_first, rope->rotary_dim);
+            DARIC_CHECK(L->k_scale == nullptr || L->k_scale_numel >= lay.H,
+                        "k_scale of job ", i, " has ", L->k_scale_numel, " entries, the layer has ",
+                        lay.H, " heads");
+            RowGeom g{};
+            std::string why;
+            DARIC_CHECK(row_geometry(L->t, L->page_first, lay, rope->rotary_dim, rope->is_neox != 0,
+                                     r.jobs[i].span, &g, &why),
+                        "fused scatter+rerotate does not support the layout of job ", i, " (",
+                        why, "); use scatter_pages followed by rerotate_pages");
+            CopyJob& j = r.jobs[i];
+            j.delta = static_cast<float>(deltas[i]);
+            j.n_tokens = static_cast<int32_t>(std::min<int64_t>(num_tokens[i], kIntMax));
+            const Key key{kind, g.W, g.n_rows, g.krows, g.tok_div, g.PS, g.H, g.R, g.ipr};
+            groups[key].push_back(i);
+            geoms[key] = g;
+        }
+        DeviceGuard guard(r.device);
+        const hipStream_t st = as_stream(stream);
+        for (const auto& [key, members] : groups) {
+            std::vector<CopyJob> gj;
+            gj.reserve(members.size());
+            int64_t max_tiles = 0;
+            for (int64_t i : members) {
+                gj.push_back(r.jobs[i]);
+                max_tiles = std::max<int64_t>(max_tiles, int64_t(r.jobs[i].prefix) * r.jobs[i].n_sel);
+            }
+            if (max_tiles == 0) continue;
+            RowGeomDiv gd;
+            gd.g = geoms[key];
+            gd.ipr = FastDiv(gd.g.ipr);
+            gd.tok_div = FastDiv(gd.g.tok_div);
+            gd.ps = FastDiv(gd.g.PS);
+            gd.h = FastDiv(gd.g.H);
+            DescUpload up(r.device, gj.data(), gj.size() * sizeof(CopyJob), st);
+            LaunchTimer timer(st);
+            launch_scatter_rotate(static_cast<const CopyJob*>(up.get()), static_cast<int>(gj.size()),
+                                  static_cast<int>(max_tiles), gd, std::get<0>(key),
+                                  rope->is_neox != 0, rope->inv_freq, st);
+        }
+    });
+}
+
+// ------------------------------------------------------------ batched memcpy
+static int batched_memcpy(const daric_tensor* dev_t, const daric_tensor* host_t,
+                          const int64_t* dev_offsets, const int64_t* host_offsets,
+                          const int64_t* sizes, int64_t n, uint64_t stream, bool d2h) {
+    return guarded([&] {
+        if (n == 0) return;
+        DARIC_CHECK(n > 0 && dev_offsets && host_offsets && sizes, "offset/size arrays must not be null");
+        check_tensor_struct(dev_t, "staging");
+        check_tensor_struct(host_t, "shm");
+        DARIC_CHECK(dev_t->device >= 0, "staging must be a device tensor");
+        DARIC_CHECK(host_t->device < 0, "shm must be a host tensor");
+        const int64_t dev_bytes = numel(*dev_t) * dev_t->elem_size;
+        const int64_t host_bytes = numel(*host_t) * host_t->elem_size;
+        for (int64_t i = 0; i < n; ++i) {
+            DARIC_CHECK(dev_offsets[i] >= 0 && host_offsets[i] >= 0 && sizes[i] >= 0,
+                        "negative offset or size at region ", i);
+            DARIC_CHECK(dev_offsets[i] <= dev_bytes && sizes[i] <= dev_bytes - dev_offsets[i],
+                        "staging range out of bounds at region ", i);
+            DARIC_CHECK(host_offsets[i] <= host_bytes && sizes[i] <= host_bytes - host_offsets[i],
+                        "shm range out of bounds at region ", i);
+        }
+        DeviceGuard guard(dev_t->device);
+        const hipStream_t st = as_stream(stream);
+        uint8_t* dv = static_cast<uint8_t*>(dev_t->data);
+        uint8_t* hv = static_cast<uint8_t*>(host_t->data);
+        for (int64_t i = 0; i < n; ++i) {
+            if (sizes[i] == 0) continue;
+            if (d2h)
+                DARIC_HIP_CHECK(hipMemcpyAsync(hv + host_offsets[i], dv + dev_offsets[i],
+                                               static_cast<size_t>(sizes[i]), hipMemcpyDeviceToHost, st));
+            else
+                DARIC_HIP_CHECK(hipMemcpyAsync(dv + dev_offsets[i], hv + host_offsets[i],
+                                               static_cast<size_t>(sizes[i]), hipMemcpyHostToDevice, st));
+        }
+    });
+}
+
+int daric_batched_memcpy_d2h(const daric_tensor* staging, const daric_tensor* shm,
+                             const int64_t* stg_offsets, const int64_t* shm_offsets,
+                             const int64_t* sizes, int64_t n, uint64_t stream) {
+    return batched_memcpy(staging, shm, stg_offsets, shm_offsets, sizes, n, stream, true);
+}
+
+int daric_batched_memcpy_h2d(const daric_tensor* shm, const daric_tensor* staging,
+                             const int64_t* shm_offsets, const int64_t* stg_offsets,
+                             const int64_t* sizes, int64_t n, uint64_t stream) {
+    return batched_memcpy(staging, shm, stg_offsets, shm_offsets, sizes, n, stream, false);
+}
+
+}  // extern "C"
+
+// ====================================================== in-place re-rotation
+namespace {
+
+// All layers of one call must share shape, strides, dtype and device.
+void check_same_layers(const daric_tensor* layers, int64_t n) {
+    const daric_tensor& a = layers[0];
+    for (int64_t i = 1; i < n; ++i) {
+        const daric_tensor& b = layers[i];
+        bool same = a.ndim == b.ndim && a.dtype == b.dtype && a.elem_size == b.elem_size &&
+                    a.device == b.device;
+        for (int d = 0; same && d < a.ndim; ++d)
+            same = a.sizes[d] == b.sizes[d] && a.strides[d] == b.strides[d];
+        DARIC_CHECK(same, "all layers of one call must share shape, strides, dtype and device; layer ", i,
+                    " differs");
+    }
+}
+
+void check_block_table(const daric_tensor* bt, int device) {
+    check_tensor_struct(bt, "block_table");
+    DARIC_CHECK(bt->device == device, "block_table must be on the layers' device");
+    DARIC_CHECK(bt->ndim == 1 && bt->dtype == DARIC_DTYPE_INT32 && is_contiguous(*bt),
+                "block_table must be a 1-D contiguous int32 tensor");
+}
+
+std::vector<uint8_t*> layer_ptrs(const daric_tensor* layers, int64_t n) {
+    std::vector<uint8_t*> v(n);
+    for (int64_t i = 0; i < n; ++i) v[i] = static_cast<uint8_t*>(layers[i].data);
+    return v;
+}
+
+}  // namespace
+
+extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers, int page_first,
+                                    const daric_tensor* block_table,
+                                    const daric_rope_segment* segments, int64_t n_segments,
+                                    const daric_rope* rope, const daric_tensor* k_scales,
+                                    uint64_t stream) {
+    return guarded([&] {
+        if (n_layers == 0 || n_segments == 0) return;
+        DARIC_CHECK(n_layers > 0 && layers != nullptr, "layers must not be empty");
+        DARIC_CHECK(n_segments > 0 && segments != nullptr, "segments must not be null");
+        check_rope(rope);
+        for (int64_t i = 0; i < n_layers; ++i) check_tensor_struct(&layers[i], "kv layer");
+        check_same_layers(layers, n_layers);
+        const daric_tensor& t = layers[0];
+        DARIC_CHECK(t.device >= 0, "KV cache tensor must be on CUDA");
+        const int kind = elem_kind(t);
+        DARIC_CHECK(kind >= 0, "unsupported KV cache dtype for rerotate");
+        const RopeLayout L = rope_layout(t, page_first != 0, rope->rotary_dim);
+        check_block_table(block_table, t.device);
+        const int64_t bt_n = numel(*block_table);
+        if (k_scales != nullptr && k_scales->data != nullptr) {
+            DARIC_CHECK(k_scales->device == t.device && k_scales->dtype == DARIC_DTYPE_FLOAT32 &&
+                        is_contiguous(*k_scales) && numel(*k_scales) == n_layers * L.H,
+                        "k_scales must be a contiguous float32 [n_layers, H] tensor on the layers' device");
+        }
+        const bool neox = rope->is_neox != 0;
+        const int64_t e = t.elem_size;
+        const int64_t VE = kind == kE4M3 ? 16 : 8;
+        const int64_t half = rope->rotary_dim / 2;
+        bool vec = (L.sb * e) % 16 == 0 && (L.ss * e) % 16 == 0 && (L.sh * e) % 16 == 0 &&
+                   (neox ? half % VE == 0 : rope->rotary_dim % VE == 0);
+        for (int64_t i = 0; i < n_layers && vec; ++i) vec = aligned(layers[i].data, 16);
+
+        InplaceGeom g{};
+        g.sb = L.sb; g.ss = L.ss; g.sh = L.sh;
+        g.PS = static_cast<int32_t>(L.PS);
+        g.H = static_cast<int32_t>(L.H);
+        g.R = rope->rotary_dim;
+        g.num_blocks = static_cast<int32_t>(L.num_blocks);
+        g.n_rot = static_cast<int32_t>(vec ? (neox ? half / VE : rope->rotary_dim / VE) : half);
+        const int64_t per_tok = L.H * g.n_rot;
+        g.tile_tokens = static_cast<int32_t>(std::max<int64_t>(1, 2048 / std::max<int64_t>(per_tok, 1)));
+
+        std::vector<RopeSeg> segs;
+        int64_t tiles = 0;
+        for (int64_t i = 0; i < n_segments; ++i) {
+            const daric_rope_segment& s = segments[i];
+            DARIC_CHECK(s.n_tokens >= 0 && s.tok_start >= 0 && s.bt_offset >= 0,
+                        "negative segment field at segment ", i);
+            DARIC_CHECK(s.delta > -(1ll << 24) && s.delta < (1ll << 24), "delta out of range at segment ", i);
+            if (s.n_tokens == 0 || s.delta == 0) continue;
+            DARIC_CHECK(s.tok_start + s.n_tokens <= kIntMax, "segment too long at segment ", i);
+            const int64_t last_block = (s.tok_start + s.n_tokens - 1) / L.PS;
+            DARIC_CHECK(s.bt_offset + last_block < bt_n, "segment ", i,
+                        " reads past the end of block_table");
+            RopeSeg rs{};
+            rs.bt_offset = s.bt_offset;
+            rs.tok_start = static_cast<int32_t>(s.tok_start);
+            rs.n_tokens = static_cast<int32_t>(s.n_tokens);
+            rs.delta = static_cast<float>(s.delta);
+            rs.tile_begin = static_cast<int32_t>(tiles);
+            tiles += (s.n_tokens + g.tile_tokens - 1) / g.tile_tokens;
+            segs.push_back(rs);
+        }
+        if (segs.empty()) return;
+        DARIC_CHECK(tiles <= kMaxTiles, "too many tokens in one rerotate call");
+        DeviceGuard guard(t.device);
+        const hipStream_t st = as_stream(stream);
+        // One upload: segments followed by the layer pointer table.
+        const size_t seg_bytes = segs.size() * sizeof(RopeSeg);
+        std::vector<uint8_t> blob(seg_bytes + n_layers * sizeof(uint8_t*));
+        std::memcpy(blob.data(), segs.data(), seg_bytes);
+        const auto ptrs = layer_ptrs(layers, n_layers);
+        std::memcpy(blob.data() + seg_bytes, ptrs.data(), n_layers * sizeof(uint8_t*));
+        DescUpload up(t.device, blob.data(), blob.size(), st);
+        const auto* d_segs = static_cast<const RopeSeg*>(up.get());
+        auto* const* d_layers = reinterpret_cast<uint8_t* const*>(static_cast<uint8_t*>(up.get()) + seg_bytes);
+        LaunchTimer timer(st);
+        launch_rerotate_inplace(d_layers, static_cast<int>(n_layers), g, d_segs,
+                                static_cast<int>(segs.size()), static_cast<int>(tiles),
+                                static_cast<const int32_t*>(block_table->data), rope->inv_freq,
+                                k_scales && k_scales->data ? static_cast<const float*>(k_scales->data) : nullptr,
+                                kind, neox, vec, st);
+    });
+}
+
+// ====================================================== recompute selection
+namespace {
+
+KVGeom kv_geom(const daric_tensor& t, bool page_first) {
+    const RopeLayout L = rope_layout(t, page_first, 2);
+    KVGeom g{};
+    g.sb = L.sb; g.ss = L.ss; g.sh = L.sh;
+    g.PS = static_cast<int32_t>(L.PS);
+    g.H = static_cast<int32_t>(L.H);
+    g.D = static_cast<int32_t>(L.D);
+    g.num_blocks = static_cast<int32_t>(L.num_blocks);
+    if (t.ndim == 5) g.v_off = page_first ? t.strides[1] : t.strides[0];
+    else if (t.ndim == 4) g.v_off = L.D;
+    else g.v_off = -1;
+    return g;
+}
+
+struct Chunks {
+    std::vector<SelChunk> v;
+    int64_t tiles = 0;
+    int64_t max_tokens = 0;
+    int64_t max_k = 0;
+};
+
+Chunks build_chunks(const daric_chunk* chunks, int64_t n, int64_t PS, int64_t bt_n, int64_t T,
+                    int tile_tokens) {
+    DARIC_CHECK(n > 0 && chunks != nullptr, "chunks must not be empty");
+    Chunks c;
+    c.v.reserve(n);
+    for (int64_t i = 0; i < n; ++i) {
+        const daric_chunk& s = chunks[i];
+        DARIC_CHECK(s.n_tokens >= 0 && s.row_offset >= 0 && s.bt_offset >= 0 && s.k >= 0,
+                    "negative chunk field at chunk ", i);
+        DARIC_CHECK(s.n_tokens <= kIntMax && s.k <= kIntMax, "chunk too long at chunk ", i);
+        DARIC_CHECK(s.row_offset + s.n_tokens <= T, "chunk ", i, " rows exceed the recomputed tensor");
+        if (s.n_tokens > 0)
+            DARIC_CHECK(s.bt_offset + (s.n_tokens - 1) / PS < bt_n, "chunk ", i,
+                        " reads past the end of block_table");
+        SelChunk sc{};
+        sc.bt_offset = s.bt_offset;
+        sc.row_offset = s.row_offset;
+        sc.n_tokens = static_cast<int32_t>(s.n_tokens);
+        sc.k = static_cast<int32_t>(s.k);
+        sc.tile_begin = static_cast<int32_t>(c.tiles);
+        c.tiles += (s.n_tokens + tile_tokens - 1) / tile_tokens;
+        c.max_tokens = std::max(c.max_tokens, s.n_tokens);
+        c.max_k = std::max(c.max_k, std::min(s.k, s.n_tokens));
+        c.v.push_back(sc);
+    }
+    return c;
+}
+
+void check_rows_tensor(const daric_tensor* x, const daric_tensor& layer, int64_t n_layers,
+                       int64_t H, int64_t D, const char* what, int64_t* T) {
+    check_tensor_struct(x, what);
+    DARIC_CHECK(x->device == layer.device, what, " must be on the layers' device");
+    DARIC_CHECK(x->ndim == 4 && x->sizes[0] == n_layers && x->sizes[2] == H && x->sizes[3] == D &&
+                is_contiguous(*x), what, " must be a contiguous [n_layers, T, H, D] tensor");
+    DARIC_CHECK(aligned(x->data, 16), what, " must be 16-byte aligned");
+    *T = x->sizes[1];
+}
+
+}  // namespace
+
+extern "C" {
+
+int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_first,
+                       const daric_tensor* block_table, const daric_tensor* k_new,
+                       const daric_chunk* chunks, int64_t n_chunks, daric_tensor* keys,
+                       uint64_t stream) {
+    return guarded([&] {
+        DARIC_CHECK(n_layers > 0 && layers != nullptr, "layers must not be empty");
+        for (int64_t i = 0; i < n_layers; ++i) check_tensor_struct(&layers[i], "kv layer");
+        check_same_layers(layers, n_layers);
+        const daric_tensor& t = layers[0];
+        DARIC_CHECK(t.device >= 0, "KV cache tensor must be on CUDA");
+        const int ck = elem_kind(t);
+        DARIC_CHECK(ck >= 0, "unsupported KV cache dtype for kv_deviation");
+        const KVGeom g = kv_geom(t, page_first != 0);
+        check_block_table(block_table, t.device);
+        int64_t T = 0;
+        check_rows_tensor(k_new, t, n_layers, g.H, g.D, "k_new", &T);
+        const int nk = k_new->dtype == DARIC_DTYPE_BFLOAT16 ? kBF16 : (k_new->dtype == DARIC_DTYPE_FLOAT16 ? kF16 : -1);
+        DARIC_CHECK(nk >= 0, "k_new must be bfloat16 or float16");
+        check_tensor_struct(keys, "keys");
+        DARIC_CHECK(keys->device == t.device && keys->dtype == DARIC_DTYPE_FLOAT32 && keys->ndim == 2 &&
+                    keys->sizes[0] == n_layers && keys->sizes[1] == T && is_contiguous(*keys),
+                    "keys must be a contiguous float32 [n_layers, T] tensor");
+        const int64_t ces = t.elem_size;
+        const int64_t need = ck == kE4M3 ? 8 : 16;
+        DARIC_CHECK(g.D % 8 == 0 && (g.sb * ces) % need == 0 && (g.ss * ces) % need == 0 &&
+                    (g.sh * ces) % need == 0 && aligned(t.data, need),
+                    "kv_deviation needs head_dim % 8 == 0 and aligned K rows");
+        for (int64_t i = 1; i < n_layers; ++i) DARIC_CHECK(aligned(layers[i].data, need), "misaligned layer ", i);
+        Chunks c = build_chunks(chunks, n_chunks, g.PS, numel(*block_table), T, 16);
+        if (c.tiles == 0) return;
+        DARIC_CHECK(c.tiles <= kMaxTiles, "too many tokens in one kv_deviation call");
+        DeviceGuard guard(t.device);
+        const hipStream_t st = as_stream(stream);
+        const size_t cb = c.v.size() * sizeof(SelChunk);
+        std::vector<uint8_t> blob(cb + n_layers * sizeof(uint8_t*));
+        std::memcpy(blob.data(), c.v.data(), cb);
+        const auto ptrs = layer_ptrs(layers, n_layers);
+        std::memcpy(blob.data() + cb, ptrs.data(), n_layers * sizeof(uint8_t*));
+        DescUpload up(t.device, blob.data(), blob.size(), st);
+        auto* const* d_layers = reinterpret_cast<uint8_t* const*>(static_cast<uint8_t*>(up.get()) + cb);
+        LaunchTimer timer(st);
+        launch_deviation(d_layers, static_cast<int>(n_layers), g, ck,
+                         static_cast<const int32_t*>(block_table->data),
+                         static_cast<const uint8_t*>(k_new->data), nk, T,
+                         static_cast<const SelChunk*>(up.get()), static_cast<int>(c.v.size()),
+                         static_cast<int>(c.tiles), nullptr, static_cast<float*>(keys->data), st);
+    });
+}
+
+int daric_topk_per_chunk(const daric_tensor* keys, const daric_chunk* chunks, int64_t n_chunks,
+                         daric_tensor* out_idx, uint64_t stream) {
+    return guarded([&] {
+        check_tensor_struct(keys, "keys");
+        DARIC_CHECK(keys->device >= 0 && keys->dtype == DARIC_DTYPE_FLOAT32 && keys->ndim == 2 &&
+                    is_contiguous(*keys), "keys must be a contiguous float32 [n_layers, T] device tensor");
+        const int64_t L = keys->sizes[0], T = keys->sizes[1];
+        check_tensor_struct(out_idx, "out_idx");
+        DARIC_CHECK(out_idx->device == keys->device && out_idx->dtype == DARIC_DTYPE_INT32 &&
+                    out_idx->ndim == 3 && out_idx->sizes[0] == L && out_idx->sizes[1] == n_chunks &&
+                    is_contiguous(*out_idx), "out_idx must be a contiguous int32 [n_layers, n_chunks, kmax] tensor");
+        const int64_t kmax = out_idx->sizes[2];
+        Chunks c = build_chunks(chunks, n_chunks, 1, kInt64Max, T, 1);
+        DARIC_CHECK(c.max_k <= kmax, "out_idx kmax (", kmax, ") is smaller than a chunk's k (", c.max_k, ")");
+        DARIC_CHECK(c.max_tokens <= 8192, "topk_per_chunk supports chunks of at most 8192 tokens");
+        DARIC_CHECK(n_chunks <= kMaxTiles && L <= 65535, "too many chunks or layers");
+        if (L == 0 || kmax == 0) return;
+        DeviceGuard guard(keys->device);
+        const hipStream_t st = as_stream(stream);
+        DescUpload up(keys->device, c.v.data(), c.v.size() * sizeof(SelChunk), st);
+        LaunchTimer timer(st);
+        launch_topk(static_cast<const float*>(keys->data), static_cast<int>(L), T,
+                    static_cast<const SelChunk*>(up.get()), static_cast<int>(n_chunks),
+                    static_cast<int>(std::max<int64_t>(c.max_tokens, 1)),
+                    static_cast<int32_t*>(out_idx->data), static_cast<int>(kmax), st);
+    });
+}
+
+int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_first,
+                     const daric_tensor* block_table, const daric_tensor* k_new,
+                     const daric_tensor* v_new, const daric_chunk* chunks, int64_t n_chunks,
+                     const daric_tensor* sel_idx, uint64_t stream) {
+    return guarded([&] {
+        DARIC_CHECK(n_layers > 0 && layers != nullptr, "layers must not be empty");
+        for (int64_t i = 0; i < n_layers; ++i) check_tensor_struct(&layers[i], "kv layer");
+        check_same_layers(layers, n_layers);
+        const daric_tensor& t = layers[0];
+        DARIC_CHECK(t.device >= 0, "KV cache tensor must be on CUDA");
+        const KVGeom g = kv_geom(t, page_first != 0);
+        check_block_table(block_table, t.device);
+        int64_t T = 0, Tv = 0;
+        check_rows_tensor(k_new, t, n_layers, g.H, g.D, "k_new", &T);
+        DARIC_CHECK(k_new->elem_size == t.elem_size, "k_new must have the cache's element size");
+        if (g.v_off >= 0) {
+            check_rows_tensor(v_new, t, n_layers, g.H, g.D, "v_new", &Tv);
+            DARIC_CHECK(Tv == T && v_new->elem_size == t.elem_size, "v_new must match k_new");
+        }
+        check_tensor_struct(sel_idx, "sel_idx");
+        DARIC_CHECK(sel_idx->device == t.device && sel_idx->dtype == DARIC_DTYPE_INT32 &&
+                    sel_idx->ndim == 3 && sel_idx->sizes[0] == n_layers &&
+                    sel_idx->sizes[1] == n_chunks && is_contiguous(*sel_idx),
+                    "sel_idx must be a contiguous int32 [n_layers, n_chunks, kmax] tensor");
+        const int64_t kmax = sel_idx->sizes[2];
+        Chunks c = build_chunks(chunks, n_chunks, g.PS, numel(*block_table), T, 1);
+        if (kmax == 0) return;
+        DARIC_CHECK(n_chunks <= 65535 && n_layers <= 65535, "too many chunks or layers for merge_rows");
+        DeviceGuard guard(t.device);
+        const hipStream_t st = as_stream(stream);
+        const size_t cb = c.v.size() * sizeof(SelChunk);
+        std::vector<uint8_t> blob(cb + n_layers * sizeof(uint8_t*));
+        std::memcpy(blob.data(), c.v.data(), cb);
+        const auto ptrs = layer_ptrs(layers, n_layers);
+        std::memcpy(blob.data() + cb, ptrs.data(), n_layers * sizeof(uint8_t*));
+        DescUpload up(t.device, blob.data(), blob.size(), st);
+        auto* const* d_layers = reinterpret_cast<uint8_t* const*>(static_cast<uint8_t*>(up.get()) + cb);
+        LaunchTimer timer(st);
+        launch_merge(d_layers, static_cast<int>(n_layers), g, t.elem_size,
+                     static_cast<const int32_t*>(block_table->data),
+                     static_cast<const uint8_t*>(k_new->data),
+                     g.v_off >= 0 ? static_cast<const uint8_t*>(v_new->data) : nullptr, T,
+                     static_cast<const SelChunk*>(up.get()), static_cast<int>(n_chunks),
+                     static_cast<const int32_t*>(sel_idx->data), static_cast<int>(kmax), st);
+    });
+}
+
+}  // extern "C"

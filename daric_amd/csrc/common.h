@@ -1,0 +1,147 @@
+// Host-side support shared by the C-ABI implementation: error state, HIP
+// error checks, tensor helpers and the per-device descriptor ring.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/daric_cache_ops.h"
+
+namespace daric {
+
+// Errors raised by host code carry the status the C ABI returns.
+struct Error : std::runtime_error {
+    int status;
+    Error(int st, const std::string& msg) : std::runtime_error(msg), status(st) {}
+};
+
+void set_last_error(const std::string& msg);
+const char* last_error();
+
+template <typename... Args>
+std::string cat(Args&&... args) {
+    std::ostringstream ss;
+    (ss << ... << args);
+    return ss.str();
+}
+
+// TORCH_CHECK counterpart: invalid argument.
+#define DARIC_CHECK(cond, ...)                                                 \
+    do {                                                                       \
+        if (!(cond)) throw ::daric::Error(DARIC_ERR_INVALID, ::daric::cat(__VA_ARGS__)); \
+    } while (0)
+
+// Reference CUDA_CHECK message format (csrc/cache_ops/cache_ops.h:12-22).
+#define DARIC_HIP_CHECK(call)                                                  \
+    do {                                                                       \
+        hipError_t err_ = (call);                                              \
+        if (err_ != hipSuccess) {                                              \
+            throw ::daric::Error(DARIC_ERR_HIP,                                \
+                ::daric::cat("HIP error at ", __FILE__, ":", __LINE__, " - ",  \
+                             hipGetErrorString(err_), " (error code ",         \
+                             static_cast<int>(err_), ")"));                    \
+        }                                                                      \
+    } while (0)
+
+// Runs `fn`, converting exceptions into a status code + thread-local message.
+template <typename F>
+int guarded(F&& fn) {
+    try {
+        fn();
+        return DARIC_OK;
+    } catch (const Error& e) {
+        set_last_error(e.what());
+        return e.status;
+    } catch (const std::bad_alloc&) {
+        set_last_error("host allocation failed");
+        return DARIC_ERR_NOMEM;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return DARIC_ERR_RUNTIME;
+    }
+}
+
+std::string fmt_dims(const int64_t* v, int n);
+inline std::string sizes_str(const daric_tensor& t) { return fmt_dims(t.sizes, t.ndim); }
+inline std::string strides_str(const daric_tensor& t) { return fmt_dims(t.strides, t.ndim); }
+
+bool is_contiguous(const daric_tensor& t);
+int64_t numel(const daric_tensor& t);
+void check_tensor_struct(const daric_tensor* t, const char* what);
+
+// Upload area for per-call job descriptors. Each device owns a ring of slots;
+// a slot pairs a pinned host buffer with a device buffer and an event recorded
+// after the launches that read it. A slot is reused only after its event has
+// completed, so concurrent calls on different streams never share live
+// descriptor memory.
+class DescRing {
+public:
+    struct Slot {
+        void* host = nullptr;
+        void* dev = nullptr;
+        size_t cap = 0;
+        hipEvent_t ev = nullptr;
+        bool pending = false;  // ev marks the last kernels that read the slot
+        bool in_use = false;   // between upload() and release()
+    };
+    static DescRing& for_device(int device);
+    // Copies `bytes` from `src` into a slot, enqueues the H2D copy on `stream`
+    // and returns the device address. The caller must call release() with
+    // the returned slot index after enqueueing every kernel that reads it.
+    void* upload(const void* src, size_t bytes, hipStream_t stream, int* slot_out);
+    void release(int slot, hipStream_t stream);
+
+private:
+    DescRing() = default;
+    static constexpr int kSlots = 16;
+    int next_ = 0;
+    Slot slots_[kSlots];
+    std::mutex mu_;
+};
+
+// RAII helper: uploads a descriptor array and releases its slot at scope exit.
+class DescUpload {
+public:
+    DescUpload(int device, const void* src, size_t bytes, hipStream_t stream)
+        : ring_(DescRing::for_device(device)), stream_(stream) {
+        ptr_ = ring_.upload(src, bytes, stream, &slot_);
+    }
+    ~DescUpload() { ring_.release(slot_, stream_); }
+    void* get() const { return ptr_; }
+
+private:
+    DescRing& ring_;
+    hipStream_t stream_;
+    int slot_ = -1;
+    void* ptr_ = nullptr;
+};
+
+// Kernel timing (daric_timing_enable / daric_timing_read).
+struct LaunchTimer {
+    hipEvent_t start = nullptr;
+    hipStream_t stream = nullptr;
+    explicit LaunchTimer(hipStream_t s);
+    ~LaunchTimer();
+};
+
+// Sets the current device for the scope and restores the previous one.
+class DeviceGuard {
+public:
+    explicit DeviceGuard(int device);
+    ~DeviceGuard();
+
+private:
+    int prev_ = -1;
+};
+
+int device_cu_count(int device);
+
+}  // namespace daric

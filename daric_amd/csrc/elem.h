@@ -1,0 +1,169 @@
+// Element types of a KV cache and their conversions to/from fp32.
+//
+// All conversions round to nearest even. The fp8 format is OCP e4m3fn
+// (bias 7, no infinities, S.1111.111 = NaN, max finite 448); fp32 -> e4m3
+// saturates to +-448 instead of producing NaN. The scalar functions compile
+// for host and device so host tests can check them exhaustively.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace daric {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+__host__ __device__ inline float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+__host__ __device__ inline uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+// ---- bf16 ----------------------------------------------------------------
+__host__ __device__ inline float bf16_to_f32(uint32_t h) { return u2f(h << 16); }
+
+__host__ __device__ inline uint32_t f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u | ((u >> 16) & 0x8000u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// ---- fp16 ----------------------------------------------------------------
+__host__ __device__ inline float f16_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+__host__ __device__ inline uint32_t f32_to_f16(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// ---- fp8 e4m3fn ------------------------------------------------------------
+__host__ __device__ inline float e4m3_to_f32(uint32_t c) {
+    const uint32_t s = (c & 0x80u) << 24;
+    const uint32_t em = c & 0x7fu;
+    if (em == 0x7fu) return u2f(s | 0x7fc00000u);
+    const uint32_t e = em >> 3, m = em & 7u;
+    if (e == 0) return u2f(s | f2u((float)m * 0.001953125f));  // m * 2^-9
+    return u2f(s | ((e + 120u) << 23) | (m << 20));
+}
+
+__host__ __device__ inline uint32_t f32_to_e4m3(float f) {
+    const uint32_t u = f2u(f);
+    const uint32_t s = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return s | 0x7fu;       // NaN
+    if (a >= 0x43e80000u) return s | 0x7eu;      // |f| >= 464 (and inf): saturate
+    if (a < 0x3c800000u) {                       // |f| < 2^-6: multiples of 2^-9
+        const float q = __builtin_rintf(u2f(a) * 512.0f);
+        return s | (uint32_t)q;                  // q == 8 is the smallest normal
+    }
+    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    uint32_t code = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+    if (code > 0x7eu) code = 0x7eu;
+    return s | code;
+}
+
+// gfx950 conversion instructions (v_cvt_pk_f32_fp8 / v_cvt_pk_fp8_f32, OCP
+// e4m3 on this target). The encoder clamps to +-448 first, so the result is
+// the saturating RTNE code for every finite input. The host pass (never
+// executed) falls back to the scalar functions.
+__device__ inline void e4m3x4_to_f32_hw(uint32_t w, float* out) {
+#ifdef __HIP_DEVICE_COMPILE__
+    auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    out[0] = lo[0]; out[1] = lo[1]; out[2] = hi[0]; out[3] = hi[1];
+#else
+    for (int b = 0; b < 4; ++b) out[b] = e4m3_to_f32((w >> (8 * b)) & 0xffu);
+#endif
+}
+__device__ inline uint32_t f32x4_to_e4m3_hw(const float* v) {
+#ifdef __HIP_DEVICE_COMPILE__
+    const float c0 = __builtin_amdgcn_fmed3f(v[0], -448.0f, 448.0f);
+    const float c1 = __builtin_amdgcn_fmed3f(v[1], -448.0f, 448.0f);
+    const float c2 = __builtin_amdgcn_fmed3f(v[2], -448.0f, 448.0f);
+    const float c3 = __builtin_amdgcn_fmed3f(v[3], -448.0f, 448.0f);
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(c0, c1, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c2, c3, w, true);
+    return (uint32_t)w;
+#else
+    return f32_to_e4m3(v[0]) | (f32_to_e4m3(v[1]) << 8) | (f32_to_e4m3(v[2]) << 16) |
+           (f32_to_e4m3(v[3]) << 24);
+#endif
+}
+
+// ---- 16-byte vector <-> fp32 lanes ----------------------------------------
+// Kind codes used as template parameters.
+enum ElemKind : int { kBF16 = 0, kF16 = 1, kE4M3 = 2 };
+
+template <int KIND> struct Elem;
+
+template <> struct Elem<kBF16> {
+    static constexpr int VE = 8;  // elements per 16 bytes
+    __device__ static inline void unpack(const u32x4& v, float* x, float) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            x[2 * w] = u2f(v[w] << 16);
+            x[2 * w + 1] = u2f(v[w] & 0xffff0000u);
+        }
+    }
+    __device__ static inline u32x4 pack(const float* x, float) {
+        u32x4 v;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) v[w] = f32_to_bf16(x[2 * w]) | (f32_to_bf16(x[2 * w + 1]) << 16);
+        return v;
+    }
+};
+
+template <> struct Elem<kF16> {
+    static constexpr int VE = 8;
+    __device__ static inline void unpack(const u32x4& v, float* x, float) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t word = v[w];
+            x[2 * w] = f16_to_f32(word & 0xffffu);
+            x[2 * w + 1] = f16_to_f32(word >> 16);
+        }
+    }
+    __device__ static inline u32x4 pack(const float* x, float) {
+        u32x4 v;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) v[w] = f32_to_f16(x[2 * w]) | (f32_to_f16(x[2 * w + 1]) << 16);
+        return v;
+    }
+};
+
+// fp8 values are dequantised as code_value * scale and requantised as
+// sat_rtne(value * (1 / scale)).
+template <> struct Elem<kE4M3> {
+    static constexpr int VE = 16;
+    __device__ static inline void unpack(const u32x4& v, float* x, float scale) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+#ifdef DARIC_FP8_SOFTWARE
+#pragma unroll
+            for (int b = 0; b < 4; ++b) x[4 * w + b] = e4m3_to_f32((v[w] >> (8 * b)) & 0xffu);
+#else
+            e4m3x4_to_f32_hw(v[w], x + 4 * w);
+#endif
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] *= scale;
+    }
+    __device__ static inline u32x4 pack(const float* x, float inv_scale) {
+        float y[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) y[i] = x[i] * inv_scale;
+        u32x4 v;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+#ifdef DARIC_FP8_SOFTWARE
+            v[w] = f32_to_e4m3(y[4 * w]) | (f32_to_e4m3(y[4 * w + 1]) << 8) |
+                   (f32_to_e4m3(y[4 * w + 2]) << 16) | (f32_to_e4m3(y[4 * w + 3]) << 24);
+#else
+            v[w] = f32x4_to_e4m3_hw(y + 4 * w);
+#endif
+        }
+        return v;
+    }
+};
+
+}  // namespace daric

@@ -1,0 +1,89 @@
+// Device-side descriptors shared by the host launchers and the kernels.
+#pragma once
+
+#include <cstdint>
+
+namespace daric {
+
+// One page-copy job: one (layer, chunk) pair, the counterpart of the
+// reference's PageCopyJobDesc (csrc/cache_ops/cache_ops.h:24-36). Byte units.
+// Tile t of the job (t < prefix * n_sel) is prefix index p = t / n_sel and
+// selected page s = t % n_sel; its staging bytes are
+// stage[(p * n_sel + s) * span, +span) and its cache bytes are
+// layer[p * prefix_stride + idx[s] * page_stride, +span).
+struct alignas(16) CopyJob {
+    uint8_t* layer;
+    uint8_t* stage;
+    const int32_t* idx;
+    const float* k_scale;     // fp8 layers: H per-head scales (nullptr = 1)
+    int64_t prefix_stride;
+    int64_t page_stride;
+    int64_t span;
+    int32_t n_sel;
+    int32_t prefix;
+    int32_t num_pages;        // page ids outside [1, num_pages) are skipped
+    int32_t n_tokens;         // fused rotate: tokens of the job to rotate
+    float delta;              // fused rotate: fp32(new_pos - old_pos)
+    int32_t pad0;
+};
+static_assert(sizeof(CopyJob) == 80, "CopyJob layout");
+
+// Row structure of a page span for the fused scatter + rotate kernel. The
+// span is n_rows rows of W elements (rows dense, W contiguous). Rows
+// [0, krows) of prefix index 0 hold K head rows: row r is token
+// (r / tok_div) % PS and head h = tok_div == 1 ? (r / PS) % H : r % H.
+// Elements [0, R) of a K row are rotated; everything else is copied.
+struct RowGeom {
+    int32_t W;         // row width in elements
+    int32_t n_rows;    // rows per page span
+    int32_t krows;     // K rows (prefix index 0 only)
+    int32_t tok_div;   // 1 (head-major rows) or H (token-major rows)
+    int32_t PS;        // tokens per page
+    int32_t H;         // heads
+    int32_t R;         // rotary dim
+    int32_t ipr;       // work items per row
+    int32_t n_rot;     // rotated items per row
+    int32_t pad0;
+};
+
+// In-place rotation geometry (elements): K element (b, s, h, d) of a layer is
+// at base + b*sb + s*ss + h*sh + d, d < R (reference adapter.py:312-364).
+struct InplaceGeom {
+    int64_t sb;
+    int64_t ss;
+    int64_t sh;
+    int32_t PS;
+    int32_t H;
+    int32_t R;
+    int32_t num_blocks;
+    int32_t n_rot;     // rotated items per head row
+    int32_t tile_tokens;
+};
+
+struct RopeSeg {
+    int64_t bt_offset;
+    int32_t tok_start;
+    int32_t n_tokens;
+    float delta;
+    int32_t tile_begin;   // first tile of this segment
+    int32_t pad0;
+    int32_t pad1;
+};
+
+// Paged K/V row geometry for the selection kernels (elements, D contiguous).
+struct KVGeom {
+    int64_t sb, ss, sh;     // block, slot, head strides
+    int64_t v_off;          // element offset of V row relative to K row (-1: no V)
+    int32_t PS, H, D, num_blocks;
+};
+
+struct SelChunk {
+    int64_t bt_offset;
+    int64_t row_offset;
+    int32_t n_tokens;
+    int32_t k;
+    int32_t tile_begin;
+    int32_t pad0;
+};
+
+}  // namespace daric

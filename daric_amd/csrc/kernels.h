@@ -1,0 +1,70 @@
+// Launchers of the gfx950 kernels (defined in the .hip files).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+#include "jobs.h"
+
+namespace daric {
+
+// Fast 32-bit division by a run-time constant d (n, d < 2^31):
+// q = (umulhi(n, m) + n) >> s with s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1.
+struct FastDiv {
+    uint32_t d = 1, m = 1, s = 0;
+    FastDiv() = default;
+    explicit FastDiv(uint32_t div) : d(div) {
+        s = 0;
+        while ((1ull << s) < div) ++s;
+        m = static_cast<uint32_t>(((1ull << 32) * ((1ull << s) - div)) / div + 1);
+    }
+#ifdef __HIPCC__
+    __host__ __device__
+#endif
+    inline uint32_t div(uint32_t n) const {
+        // (n * m) >> 32 lowers to v_mul_hi_u32 on the device.
+        const uint32_t hi = static_cast<uint32_t>((static_cast<uint64_t>(n) * m) >> 32);
+        return (hi + n) >> s;
+    }
+};
+
+struct RowGeomDiv {
+    RowGeom g;
+    FastDiv ipr, tok_div, ps, h;
+};
+
+// Plain page copies. vw is the access width in bytes (16, 4 or 1).
+void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int vw, bool gather,
+                       hipStream_t stream);
+
+// Fused scatter + K re-rotation; kind is an ElemKind. All jobs share `geom`.
+void launch_scatter_rotate(const CopyJob* d_jobs, int n_jobs, int max_tiles,
+                           const RowGeomDiv& geom, int kind, bool neox, const float* inv_freq,
+                           hipStream_t stream);
+
+// In-place K re-rotation over segments of tokens. `layers` is a device array
+// of n_layers K base pointers; `vec` selects 16-byte (true) or per-element
+// (false) access.
+void launch_rerotate_inplace(uint8_t* const* d_layers, int n_layers, const InplaceGeom& g,
+                             const RopeSeg* d_segs, int n_segs, int n_tiles,
+                             const int32_t* block_table, const float* inv_freq,
+                             const float* k_scales, int kind, bool neox, bool vec,
+                             hipStream_t stream);
+
+// Selection kernels.
+void launch_deviation(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int cache_kind,
+                      const int32_t* block_table, const uint8_t* k_new, int new_kind,
+                      int64_t T, const SelChunk* d_chunks, int n_chunks, int n_tiles,
+                      const float* k_scales, float* keys, hipStream_t stream);
+void launch_topk(const float* keys, int n_layers, int64_t T, const SelChunk* d_chunks,
+                 int n_chunks, int max_tokens, int32_t* out_idx, int kmax, hipStream_t stream);
+void launch_merge(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int elem_size,
+                  const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,
+                  int64_t T, const SelChunk* d_chunks, int n_chunks, const int32_t* sel_idx,
+                  int kmax, hipStream_t stream);
+
+// Launch-configuration error check after a <<<>>> launch.
+void check_launch(const char* what);
+
+}  // namespace daric

@@ -1,0 +1,215 @@
+// In-place re-rotation of cached K rows (gfx950): the counterpart of the
+// reference's Triton _fused_rerotate_kernel (daric/adaption/adapter.py:30-88).
+//
+// The reference launches one program per (token, head) with a per-token
+// cos/sin table read from HBM. Here a workgroup takes a tile of tokens of one
+// segment (a run of tokens that all move by the same delta), computes the
+// segment's rotary_dim/2 cos/sin values once in fp32 into LDS, and streams
+// the tile's K head rows with 16-byte accesses (per-element accesses when the
+// layout is not 16-byte aligned). Only the rotated [0, R) part of each head
+// row is read and written; V and the rotary tail are never touched.
+#include <hip/hip_runtime.h>
+
+#include "elem.h"
+#include "jobs.h"
+#include "kernels.h"
+
+namespace daric {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+constexpr int kMaxHalfRot = 256;
+
+__device__ __forceinline__ int find_segment(const RopeSeg* __restrict__ segs, int n, int tile) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (segs[mid].tile_begin <= tile) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+__device__ __forceinline__ void fill_cos_sin(float* s_cos, float* s_sin, int half, float delta,
+                                             const float* __restrict__ inv_freq) {
+    for (int i = threadIdx.x; i < half; i += kThreads) {
+        float sn, cs;
+        sincosf(delta * inv_freq[i], &sn, &cs);
+        s_cos[i] = cs;
+        s_sin[i] = sn;
+    }
+    __syncthreads();
+}
+
+template <int KIND, bool NEOX>
+__global__ __launch_bounds__(kThreads) void rerotate_vec_kernel(
+    uint8_t* const* __restrict__ layers, InplaceGeom g, const RopeSeg* __restrict__ segs,
+    int n_segs, const int32_t* __restrict__ bt, const float* __restrict__ inv_freq,
+    const float* __restrict__ k_scales) {
+    using E = Elem<KIND>;
+    constexpr int VE = E::VE;
+    constexpr int ES = KIND == kE4M3 ? 1 : 2;
+    __shared__ float s_cos[kMaxHalfRot];
+    __shared__ float s_sin[kMaxHalfRot];
+
+    const int tile = static_cast<int>(blockIdx.x);
+    const RopeSeg& sg = segs[find_segment(segs, n_segs, tile)];
+    const int tok0 = (tile - sg.tile_begin) * g.tile_tokens;
+    const int n_tok = min(g.tile_tokens, sg.n_tokens - tok0);
+    if (n_tok <= 0 || sg.delta == 0.0f) return;
+    const int half = g.R / 2;
+    fill_cos_sin(s_cos, s_sin, half, sg.delta, inv_freq);
+
+    uint8_t* __restrict__ base = layers[blockIdx.y];
+    const float* ksc = k_scales ? k_scales + static_cast<int64_t>(blockIdx.y) * g.H : nullptr;
+    const int per_tok = g.H * g.n_rot;
+    const int items = n_tok * per_tok;
+    const int64_t partner_b = NEOX ? static_cast<int64_t>(half) * ES : 0;
+
+    for (int b0 = 0; b0 < items; b0 += kThreads * kUnroll) {
+        u32x4 a[kUnroll], bb[kUnroll];
+        int64_t off[kUnroll];
+        int kk[kUnroll], hh[kUnroll];
+        bool ok[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int it = b0 + u * kThreads + static_cast<int>(threadIdx.x);
+            const int t = it / per_tok;
+            const int rem = it - t * per_tok;
+            const int h = rem / g.n_rot;
+            const int k = rem - h * g.n_rot;
+            const int pos = sg.tok_start + tok0 + t;
+            int blk = -1;
+            if (it < items) blk = bt[sg.bt_offset + pos / g.PS];
+            ok[u] = it < items && blk >= 0 && blk < g.num_blocks;
+            kk[u] = k;
+            hh[u] = h;
+            off[u] = (static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(pos % g.PS) * g.ss +
+                      static_cast<int64_t>(h) * g.sh + static_cast<int64_t>(k) * VE) * ES;
+            if (ok[u]) {
+                a[u] = *reinterpret_cast<const u32x4*>(base + off[u]);
+                if (NEOX) bb[u] = *reinterpret_cast<const u32x4*>(base + off[u] + partner_b);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (!ok[u]) continue;
+            const float scale = (KIND == kE4M3 && ksc) ? ksc[hh[u]] : 1.0f;
+            const float inv = 1.0f / scale;
+            float x[VE];
+            E::unpack(a[u], x, scale);
+            if (NEOX) {
+                float y[VE];
+                E::unpack(bb[u], y, scale);
+                const int i0 = kk[u] * VE;
+#pragma unroll
+                for (int e = 0; e < VE; ++e) {
+                    const float c = s_cos[i0 + e], sn = s_sin[i0 + e];
+                    const float x1 = x[e], x2 = y[e];
+                    x[e] = x1 * c - x2 * sn;
+                    y[e] = x2 * c + x1 * sn;
+                }
+                *reinterpret_cast<u32x4*>(base + off[u]) = E::pack(x, inv);
+                *reinterpret_cast<u32x4*>(base + off[u] + partner_b) = E::pack(y, inv);
+            } else {
+                const int i0 = kk[u] * (VE / 2);
+#pragma unroll
+                for (int m = 0; m < VE / 2; ++m) {
+                    const float c = s_cos[i0 + m], sn = s_sin[i0 + m];
+                    const float x1 = x[2 * m], x2 = x[2 * m + 1];
+                    x[2 * m] = x1 * c - x2 * sn;
+                    x[2 * m + 1] = x2 * c + x1 * sn;
+                }
+                *reinterpret_cast<u32x4*>(base + off[u]) = E::pack(x, inv);
+            }
+        }
+    }
+}
+
+// Per-element variant for layouts whose rows or pair halves are not 16-byte
+// aligned. One item = one rotation pair.
+template <int KIND>
+__device__ __forceinline__ float load_elem(const uint8_t* p, float scale) {
+    if (KIND == kBF16) return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+    if (KIND == kF16) return f16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+    return e4m3_to_f32(*p) * scale;
+}
+template <int KIND>
+__device__ __forceinline__ void store_elem(uint8_t* p, float v, float inv) {
+    if (KIND == kBF16) *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(f32_to_bf16(v));
+    else if (KIND == kF16) *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(f32_to_f16(v));
+    else *p = static_cast<uint8_t>(f32_to_e4m3(v * inv));
+}
+
+template <int KIND, bool NEOX>
+__global__ __launch_bounds__(kThreads) void rerotate_elem_kernel(
+    uint8_t* const* __restrict__ layers, InplaceGeom g, const RopeSeg* __restrict__ segs,
+    int n_segs, const int32_t* __restrict__ bt, const float* __restrict__ inv_freq,
+    const float* __restrict__ k_scales) {
+    constexpr int ES = KIND == kE4M3 ? 1 : 2;
+    __shared__ float s_cos[kMaxHalfRot];
+    __shared__ float s_sin[kMaxHalfRot];
+    const int tile = static_cast<int>(blockIdx.x);
+    const RopeSeg& sg = segs[find_segment(segs, n_segs, tile)];
+    const int tok0 = (tile - sg.tile_begin) * g.tile_tokens;
+    const int n_tok = min(g.tile_tokens, sg.n_tokens - tok0);
+    if (n_tok <= 0 || sg.delta == 0.0f) return;
+    const int half = g.R / 2;
+    fill_cos_sin(s_cos, s_sin, half, sg.delta, inv_freq);
+    uint8_t* __restrict__ base = layers[blockIdx.y];
+    const float* ksc = k_scales ? k_scales + static_cast<int64_t>(blockIdx.y) * g.H : nullptr;
+    const int per_tok = g.H * half;
+    const int items = n_tok * per_tok;
+    for (int it = threadIdx.x; it < items; it += kThreads) {
+        const int t = it / per_tok;
+        const int rem = it - t * per_tok;
+        const int h = rem / half;
+        const int i = rem - h * half;
+        const int pos = sg.tok_start + tok0 + t;
+        const int blk = bt[sg.bt_offset + pos / g.PS];
+        if (blk < 0 || blk >= g.num_blocks) continue;
+        const int64_t row = static_cast<int64_t>(blk) * g.sb +
+                            static_cast<int64_t>(pos % g.PS) * g.ss + static_cast<int64_t>(h) * g.sh;
+        const int64_t e1 = NEOX ? row + i : row + 2 * i;
+        const int64_t e2 = NEOX ? row + i + half : row + 2 * i + 1;
+        const float scale = (KIND == kE4M3 && ksc) ? ksc[h] : 1.0f;
+        const float x1 = load_elem<KIND>(base + e1 * ES, scale);
+        const float x2 = load_elem<KIND>(base + e2 * ES, scale);
+        const float c = s_cos[i], sn = s_sin[i];
+        store_elem<KIND>(base + e1 * ES, x1 * c - x2 * sn, 1.0f / scale);
+        store_elem<KIND>(base + e2 * ES, x2 * c + x1 * sn, 1.0f / scale);
+    }
+}
+
+}  // namespace
+
+void launch_rerotate_inplace(uint8_t* const* d_layers, int n_layers, const InplaceGeom& g,
+                             const RopeSeg* d_segs, int n_segs, int n_tiles,
+                             const int32_t* block_table, const float* inv_freq,
+                             const float* k_scales, int kind, bool neox, bool vec,
+                             hipStream_t stream) {
+    constexpr int kMaxY = 65535;
+    for (int l0 = 0; l0 < n_layers; l0 += kMaxY) {
+        const int nl = n_layers - l0 < kMaxY ? n_layers - l0 : kMaxY;
+        const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(nl));
+        uint8_t* const* lp = d_layers + l0;
+        const float* ks = k_scales ? k_scales + static_cast<int64_t>(l0) * g.H : nullptr;
+#define DARIC_RV(K, N) rerotate_vec_kernel<K, N><<<grid, kThreads, 0, stream>>>(lp, g, d_segs, n_segs, block_table, inv_freq, ks)
+#define DARIC_RE(K, N) rerotate_elem_kernel<K, N><<<grid, kThreads, 0, stream>>>(lp, g, d_segs, n_segs, block_table, inv_freq, ks)
+        if (vec) {
+            if (kind == kBF16) { if (neox) DARIC_RV(kBF16, true); else DARIC_RV(kBF16, false); }
+            else if (kind == kF16) { if (neox) DARIC_RV(kF16, true); else DARIC_RV(kF16, false); }
+            else { if (neox) DARIC_RV(kE4M3, true); else DARIC_RV(kE4M3, false); }
+        } else {
+            if (kind == kBF16) { if (neox) DARIC_RE(kBF16, true); else DARIC_RE(kBF16, false); }
+            else if (kind == kF16) { if (neox) DARIC_RE(kF16, true); else DARIC_RE(kF16, false); }
+            else { if (neox) DARIC_RE(kE4M3, true); else DARIC_RE(kE4M3, false); }
+        }
+#undef DARIC_RV
+#undef DARIC_RE
+        check_launch("rerotate_pages");
+    }
+}
+
+}  // namespace daric

@@ -1,0 +1,194 @@
+// Host runtime support: error state, tensor helpers, descriptor ring, timing.
+#include <atomic>
+#include <map>
+#include <memory>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace daric {
+
+namespace {
+thread_local std::string g_last_error;
+std::atomic<bool> g_timing{false};
+std::mutex g_timing_mu;
+struct TimedLaunch {
+    hipEvent_t start, stop;
+};
+std::vector<TimedLaunch> g_timed;
+}  // namespace
+
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+const char* last_error() { return g_last_error.c_str(); }
+
+std::string fmt_dims(const int64_t* v, int n) {
+    std::ostringstream ss;
+    ss << "[";
+    for (int i = 0; i < n; ++i) ss << (i ? ", " : "") << v[i];
+    ss << "]";
+    return ss.str();
+}
+
+bool is_contiguous(const daric_tensor& t) {
+    int64_t expected = 1;
+    for (int d = t.ndim - 1; d >= 0; --d) {
+        if (t.sizes[d] == 1) continue;
+        if (t.strides[d] != expected) return false;
+        expected *= t.sizes[d];
+    }
+    return true;
+}
+
+int64_t numel(const daric_tensor& t) {
+    int64_t n = 1;
+    for (int d = 0; d < t.ndim; ++d) n *= t.sizes[d];
+    return n;
+}
+
+void check_tensor_struct(const daric_tensor* t, const char* what) {
+    DARIC_CHECK(t != nullptr, what, " must not be null");
+    DARIC_CHECK(t->ndim >= 0 && t->ndim <= DARIC_MAX_DIMS, what, " has an invalid rank: ", t->ndim);
+    DARIC_CHECK(t->elem_size > 0, what, " has an invalid element size");
+}
+
+void check_launch(const char* what) {
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        throw Error(DARIC_ERR_HIP, cat("HIP error launching ", what, " - ", hipGetErrorString(err),
+                                       " (error code ", static_cast<int>(err), ")"));
+}
+
+DeviceGuard::DeviceGuard(int device) {
+    DARIC_HIP_CHECK(hipGetDevice(&prev_));
+    if (prev_ != device) DARIC_HIP_CHECK(hipSetDevice(device));
+}
+DeviceGuard::~DeviceGuard() {
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur != prev_ && prev_ >= 0) (void)hipSetDevice(prev_);
+}
+
+int device_cu_count(int device) {
+    int n = 0;
+    DARIC_HIP_CHECK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device));
+    return n;
+}
+
+// ---------------------------------------------------------------- DescRing
+DescRing& DescRing::for_device(int device) {
+    static std::mutex mu;
+    static std::map<int, std::unique_ptr<DescRing>> rings;
+    std::lock_guard<std::mutex> lk(mu);
+    auto& r = rings[device];
+    if (!r) r.reset(new DescRing());
+    return *r;
+}
+
+void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* slot_out) {
+    std::unique_lock<std::mutex> lk(mu_);
+    // A slot between upload() and release() belongs to a call that is still
+    // enqueueing kernels on it; skip such slots (wait if all are taken).
+    int idx = -1;
+    for (;;) {
+        for (int k = 0; k < kSlots; ++k) {
+            const int c = (next_ + k) % kSlots;
+            if (!slots_[c].in_use) { idx = c; break; }
+        }
+        if (idx >= 0) break;
+        lk.unlock();
+        std::this_thread::yield();
+        lk.lock();
+    }
+    next_ = (idx + 1) % kSlots;
+    Slot& s = slots_[idx];
+    s.in_use = true;
+    if (s.pending) {
+        DARIC_HIP_CHECK(hipEventSynchronize(s.ev));
+        s.pending = false;
+    }
+    if (s.ev == nullptr) DARIC_HIP_CHECK(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
+    if (bytes > s.cap) {
+        size_t cap = 4096;
+        while (cap < bytes) cap *= 2;
+        if (s.host) DARIC_HIP_CHECK(hipHostFree(s.host));
+        if (s.dev) DARIC_HIP_CHECK(hipFree(s.dev));
+        s.host = nullptr;
+        s.dev = nullptr;
+        s.cap = 0;
+        DARIC_HIP_CHECK(hipHostMalloc(&s.host, cap, hipHostMallocDefault));
+        DARIC_HIP_CHECK(hipMalloc(&s.dev, cap));
+        s.cap = cap;
+    }
+    *slot_out = idx;
+    try {
+        std::memcpy(s.host, src, bytes);
+        DARIC_HIP_CHECK(hipMemcpyAsync(s.dev, s.host, bytes, hipMemcpyHostToDevice, stream));
+    } catch (...) {
+        s.in_use = false;
+        throw;
+    }
+    return s.dev;
+}
+
+void DescRing::release(int slot, hipStream_t stream) {
+    if (slot < 0) return;
+    std::lock_guard<std::mutex> lk(mu_);
+    Slot& s = slots_[slot];
+    // The event marks the end of every kernel that reads the slot; if it
+    // cannot be recorded, wait for the stream instead so reuse stays safe.
+    if (hipEventRecord(s.ev, stream) == hipSuccess) s.pending = true;
+    else (void)hipStreamSynchronize(stream);
+    s.in_use = false;
+}
+
+// ---------------------------------------------------------------- timing
+LaunchTimer::LaunchTimer(hipStream_t s) : stream(s) {
+    if (!g_timing.load(std::memory_order_relaxed)) return;
+    DARIC_HIP_CHECK(hipEventCreate(&start));
+    DARIC_HIP_CHECK(hipEventRecord(start, stream));
+}
+
+LaunchTimer::~LaunchTimer() {
+    if (start == nullptr) return;
+    hipEvent_t stop = nullptr;
+    if (hipEventCreate(&stop) != hipSuccess) return;
+    if (hipEventRecord(stop, stream) != hipSuccess) return;
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    g_timed.push_back({start, stop});
+}
+
+}  // namespace daric
+
+using namespace daric;
+
+extern "C" {
+
+int daric_abi_version(void) { return DARIC_ABI_VERSION; }
+
+const char* daric_last_error(void) { return daric::last_error(); }
+
+int daric_timing_enable(int enable) {
+    return guarded([&] { g_timing.store(enable != 0); });
+}
+
+int daric_timing_read(double* total_ms, int64_t* launches) {
+    return guarded([&] {
+        std::vector<TimedLaunch> v;
+        {
+            std::lock_guard<std::mutex> lk(g_timing_mu);
+            v.swap(g_timed);
+        }
+        double sum = 0.0;
+        for (auto& t : v) {
+            DARIC_HIP_CHECK(hipEventSynchronize(t.stop));
+            float ms = 0.0f;
+            DARIC_HIP_CHECK(hipEventElapsedTime(&ms, t.start, t.stop));
+            sum += ms;
+            (void)hipEventDestroy(t.start);
+            (void)hipEventDestroy(t.stop);
+        }
+        if (total_ms) *total_ms = sum;
+        if (launches) *launches = static_cast<int64_t>(v.size());
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,335 @@
+// Recompute selection kernels (gfx950): per-token K deviation, per-chunk
+// top-k by LDS radix select, and the merge of recomputed rows.
+//
+// Deviation order (the keys are bit-exact against the CPU oracle, which sums
+// in exactly this order): a wavefront owns one token; the token's H*D
+// elements, in (h, d) order, are cut into vectors of 8 elements; vector v is
+// loaded by lane v % 64 in round v / 64; each lane accumulates
+// acc = acc + diff * diff element by element (float32, no contraction),
+// rounds ascending; the 64 lane sums are then combined by a butterfly over
+// xor offsets 32, 16, 8, 4, 2, 1. Any NaN key is stored as 0x7FC00000.
+//
+// Top-k ranks keys by the IEEE total order of their float32 bits (NaN above
+// +inf), ties to the lower token index, and writes the selected chunk-local
+// indices in ascending order.
+#include <hip/hip_runtime.h>
+
+#include "elem.h"
+#include "jobs.h"
+#include "kernels.h"
+
+namespace daric {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kTokPerWave = 4;
+constexpr int kTileTokens = kWaves * kTokPerWave;  // tokens per deviation workgroup
+constexpr int kMergeTok = 8;                       // selected tokens per merge workgroup
+
+__device__ __forceinline__ int find_chunk(const SelChunk* __restrict__ ch, int n, int tile) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (ch[mid].tile_begin <= tile) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// 8 elements starting at p (16 bytes for 2-byte types, 8 bytes for fp8).
+template <int KIND>
+__device__ __forceinline__ void load8(const uint8_t* p, float* x, float scale) {
+    if (KIND == kE4M3) {
+        const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+#ifdef DARIC_FP8_SOFTWARE
+#pragma unroll
+        for (int b = 0; b < 4; ++b) { x[b] = e4m3_to_f32((w[0] >> (8 * b)) & 0xffu); x[4 + b] = e4m3_to_f32((w[1] >> (8 * b)) & 0xffu); }
+#else
+        e4m3x4_to_f32_hw(w[0], x);
+        e4m3x4_to_f32_hw(w[1], x + 4);
+#endif
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = x[i] * scale;
+    } else {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (KIND == kBF16) {
+                x[2 * q] = u2f(w[q] << 16);
+                x[2 * q + 1] = u2f(w[q] & 0xffff0000u);
+            } else {
+                const uint32_t word = w[q];
+                x[2 * q] = f16_to_f32(word & 0xffffu);
+                x[2 * q + 1] = f16_to_f32(word >> 16);
+            }
+        }
+    }
+}
+
+template <int CK, int NK>
+__global__ __launch_bounds__(kThreads) void deviation_kernel(
+    uint8_t* const* __restrict__ layers, KVGeom g, const int32_t* __restrict__ bt,
+    const uint8_t* __restrict__ k_new, int64_t T, const SelChunk* __restrict__ chunks,
+    int n_chunks, const float* __restrict__ k_scales, float* __restrict__ keys) {
+#pragma clang fp contract(off)
+    constexpr int CES = CK == kE4M3 ? 1 : 2;
+    const int l = static_cast<int>(blockIdx.y);
+    const int tile = static_cast<int>(blockIdx.x);
+    const SelChunk& c = chunks[find_chunk(chunks, n_chunks, tile)];
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const int j0 = (tile - c.tile_begin) * kTileTokens + wave * kTokPerWave;
+    const int N = g.H * g.D;
+    const int n_vec = N >> 3;
+    const int rounds = (n_vec + 63) >> 6;
+    const uint8_t* __restrict__ base = layers[l];
+    const float* ksc = k_scales ? k_scales + static_cast<int64_t>(l) * g.H : nullptr;
+
+    int64_t cache_row[kTokPerWave];
+    const uint8_t* new_row[kTokPerWave];
+    bool valid[kTokPerWave];
+#pragma unroll
+    for (int i = 0; i < kTokPerWave; ++i) {
+        const int j = j0 + i;
+        int blk = -1;
+        if (j < c.n_tokens) blk = bt[c.bt_offset + j / g.PS];
+        valid[i] = j < c.n_tokens && blk >= 0 && blk < g.num_blocks;
+        cache_row[i] = static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(j % g.PS) * g.ss;
+        new_row[i] = k_new + ((static_cast<int64_t>(l) * T + c.row_offset + j) * N) * 2;
+    }
+
+    float acc[kTokPerWave];
+#pragma unroll
+    for (int i = 0; i < kTokPerWave; ++i) acc[i] = 0.0f;
+
+    for (int r = 0; r < rounds; ++r) {
+        const int v = r * 64 + lane;
+        if (v >= n_vec) break;
+        const int e0 = v << 3;
+        const int h = e0 / g.D;
+        const int d0 = e0 - h * g.D;
+        const float scale = (CK == kE4M3 && ksc) ? ksc[h] : 1.0f;
+        float a[kTokPerWave][8], b[kTokPerWave][8];
+#pragma unroll
+        for (int i = 0; i < kTokPerWave; ++i) {
+            if (!valid[i]) continue;
+            load8<NK>(new_row[i] + static_cast<int64_t>(e0) * 2, a[i], 1.0f);
+            load8<CK>(base + (cache_row[i] + static_cast<int64_t>(h) * g.sh + d0) * CES, b[i], scale);
+        }
+#pragma unroll
+        for (int i = 0; i < kTokPerWave; ++i) {
+            if (!valid[i]) continue;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = a[i][e] - b[i][e];
+                const float sq = d * d;
+                acc[i] = acc[i] + sq;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kTokPerWave; ++i) {
+        float s = acc[i];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, 64);
+        const int j = j0 + i;
+        if (lane == 0 && j < c.n_tokens) {
+            float key = valid[i] ? s : 0.0f;
+            if (key != key) key = u2f(0x7fc00000u);
+            keys[static_cast<int64_t>(l) * T + c.row_offset + j] = key;
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+    uint32_t b = f2u(f);
+    if ((b & 0x7fffffffu) > 0x7f800000u) b = 0x7fc00000u;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Exclusive prefix count of `flag` over the workgroup; *total gets the sum.
+__device__ __forceinline__ int block_excl_count(bool flag, int* s_wave, int* total) {
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const unsigned long long m = __ballot(flag);
+    const int below = __popcll(m & ((1ull << lane) - 1ull));
+    if (lane == 0) s_wave[wave] = __popcll(m);
+    __syncthreads();
+    int before = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const int cnt = s_wave[w];
+        before += w < wave ? cnt : 0;
+        sum += cnt;
+    }
+    __syncthreads();
+    *total = sum;
+    return before + below;
+}
+
+__global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ keys, int64_t T,
+                                                        const SelChunk* __restrict__ chunks,
+                                                        int n_chunks, int32_t* __restrict__ out,
+                                                        int kmax) {
+    extern __shared__ uint32_t s_keys[];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_digit, s_above;
+    __shared__ int s_wave[kWaves];
+
+    const int l = static_cast<int>(blockIdx.y);
+    const int ci = static_cast<int>(blockIdx.x);
+    const SelChunk& c = chunks[ci];
+    const int n = c.n_tokens;
+    const int k = min(max(c.k, 0), n);
+    int32_t* __restrict__ orow = out + (static_cast<int64_t>(l) * n_chunks + ci) * kmax;
+    const int tid = static_cast<int>(threadIdx.x);
+
+    for (int i = k + tid; i < kmax; i += kThreads) orow[i] = -1;
+    if (k == 0) return;
+    const float* krow = keys + static_cast<int64_t>(l) * T + c.row_offset;
+    for (int i = tid; i < n; i += kThreads) s_keys[i] = order_key(krow[i]);
+
+    uint32_t prefix = 0, mask = 0, krem = static_cast<uint32_t>(k);
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        hist[tid] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += kThreads) {
+            const uint32_t key = s_keys[i];
+            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        // suffix sums over digits (from 255 down): thread t holds digit 255 - t
+        const uint32_t cnt = hist[255 - tid];
+        uint32_t incl = cnt;
+        const int lane = tid & 63;
+        const int wave = tid >> 6;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        if (lane == 63) s_wave[wave] = static_cast<int>(incl);
+        __syncthreads();
+        uint32_t before = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) before += w < wave ? static_cast<uint32_t>(s_wave[w]) : 0u;
+        incl += before;
+        const uint32_t excl = incl - cnt;  // keys with a larger digit
+        if (excl < krem && incl >= krem) {
+            s_digit = static_cast<uint32_t>(255 - tid);
+            s_above = excl;
+        }
+        __syncthreads();
+        prefix |= s_digit << shift;
+        mask |= 255u << shift;
+        krem -= s_above;
+        __syncthreads();
+    }
+    // prefix is the k-th largest key; take every larger key and the first
+    // krem keys equal to it, in index order.
+    int running = 0, eq_seen = 0;
+    for (int b = 0; b < n; b += kThreads) {
+        const int i = b + tid;
+        const uint32_t key = i < n ? s_keys[i] : 0u;
+        const bool gt = i < n && key > prefix;
+        const bool eq = i < n && key == prefix;
+        int eq_total, sel_total;
+        const int eq_rank = eq_seen + block_excl_count(eq, s_wave, &eq_total);
+        const bool sel = gt || (eq && eq_rank < static_cast<int>(krem));
+        const int pos = running + block_excl_count(sel, s_wave, &sel_total);
+        if (sel && pos < k) orow[pos] = i;
+        running += sel_total;
+        eq_seen += eq_total;
+    }
+}
+
+template <int VW>
+__global__ __launch_bounds__(kThreads) void merge_kernel(
+    uint8_t* const* __restrict__ layers, KVGeom g, int es, const int32_t* __restrict__ bt,
+    const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T,
+    const SelChunk* __restrict__ chunks, int n_chunks, const int32_t* __restrict__ sel, int kmax) {
+    using V = typename std::conditional<VW == 16, u32x4, uint8_t>::type;
+    const int l = static_cast<int>(blockIdx.z);
+    const int ci = static_cast<int>(blockIdx.y);
+    const SelChunk& c = chunks[ci];
+    const int q0 = static_cast<int>(blockIdx.x) * kMergeTok;
+    const int32_t* srow = sel + (static_cast<int64_t>(l) * n_chunks + ci) * kmax;
+    uint8_t* __restrict__ base = layers[l];
+    const int upr = g.D * es / VW;               // units per head row
+    const int per_tok = 2 * g.H * upr;           // K and V rows
+    const int items = kMergeTok * per_tok;
+    const int64_t rowbytes = static_cast<int64_t>(g.H) * g.D * es;
+    for (int it = threadIdx.x; it < items; it += kThreads) {
+        const int t = it / per_tok;
+        int rem = it - t * per_tok;
+        const int kv = rem / (g.H * upr);
+        rem -= kv * g.H * upr;
+        const int h = rem / upr;
+        const int u = rem - h * upr;
+        const int q = q0 + t;
+        if (q >= kmax || q >= c.k) continue;
+        const int j = srow[q];
+        if (j < 0 || j >= c.n_tokens) continue;
+        if (kv == 1 && g.v_off < 0) continue;
+        const int blk = bt[c.bt_offset + j / g.PS];
+        if (blk <= 0 || blk >= g.num_blocks) continue;
+        const int64_t dst_el = static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(j % g.PS) * g.ss +
+                               static_cast<int64_t>(h) * g.sh + (kv ? g.v_off : 0);
+        const uint8_t* src = (kv ? v_new : k_new) +
+                             (static_cast<int64_t>(l) * T + c.row_offset + j) * rowbytes +
+                             static_cast<int64_t>(h) * g.D * es;
+        *reinterpret_cast<V*>(base + dst_el * es + static_cast<int64_t>(u) * VW) =
+            *reinterpret_cast<const V*>(src + static_cast<int64_t>(u) * VW);
+    }
+}
+
+}  // namespace
+
+void launch_deviation(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int cache_kind,
+                      const int32_t* block_table, const uint8_t* k_new, int new_kind,
+                      int64_t T, const SelChunk* d_chunks, int n_chunks, int n_tiles,
+                      const float* k_scales, float* keys, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_layers));
+#define DARIC_DV(C, N) deviation_kernel<C, N><<<grid, kThreads, 0, stream>>>(d_layers, g, block_table, k_new, T, d_chunks, n_chunks, k_scales, keys)
+    if (new_kind == kBF16) {
+        if (cache_kind == kBF16) DARIC_DV(kBF16, kBF16);
+        else if (cache_kind == kF16) DARIC_DV(kF16, kBF16);
+        else DARIC_DV(kE4M3, kBF16);
+    } else {
+        if (cache_kind == kBF16) DARIC_DV(kBF16, kF16);
+        else if (cache_kind == kF16) DARIC_DV(kF16, kF16);
+        else DARIC_DV(kE4M3, kF16);
+    }
+#undef DARIC_DV
+    check_launch("kv_deviation");
+}
+
+void launch_topk(const float* keys, int n_layers, int64_t T, const SelChunk* d_chunks,
+                 int n_chunks, int max_tokens, int32_t* out_idx, int kmax, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
+    const size_t lds = static_cast<size_t>(max_tokens) * sizeof(uint32_t);
+    topk_kernel<<<grid, kThreads, lds, stream>>>(keys, T, d_chunks, n_chunks, out_idx, kmax);
+    check_launch("topk_per_chunk");
+}
+
+void launch_merge(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int elem_size,
+                  const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,
+                  int64_t T, const SelChunk* d_chunks, int n_chunks, const int32_t* sel_idx,
+                  int kmax, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((kmax + kMergeTok - 1) / kMergeTok),
+                    static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
+    const bool vec = (g.D * elem_size) % 16 == 0 && (g.sb * elem_size) % 16 == 0 &&
+                     (g.ss * elem_size) % 16 == 0 && (g.sh * elem_size) % 16 == 0 &&
+                     (g.v_off < 0 || (g.v_off * elem_size) % 16 == 0);
+    if (vec)
+        merge_kernel<16><<<grid, kThreads, 0, stream>>>(d_layers, g, elem_size, block_table, k_new,
+                                                        v_new, T, d_chunks, n_chunks, sel_idx, kmax);
+    else
+        merge_kernel<1><<<grid, kThreads, 0, stream>>>(d_layers, g, elem_size, block_table, k_new,
+                                                       v_new, T, d_chunks, n_chunks, sel_idx, kmax);
+    check_launch("merge_rows");
+}
+
+}  // namespace daric

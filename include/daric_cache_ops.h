@@ -1,0 +1,247 @@
+/*
+ * daric_cache_ops.h -- C ABI of the MI355X (gfx950) KV-reuse hot path.
+ *
+ * This library replaces the reference's pybind11 module `daric.cache_ops`
+ * (reference: csrc/cache_ops/bindings.cpp:7-31, stub daric/cache_ops.pyi:1-53)
+ * and the Triton re-rotation kernel (daric/adaption/adapter.py:30-88), and adds
+ * the entry points the reference lacks (fused scatter+re-rotate, fp8
+ * dequant->rotate->requant, recompute selection and merge).
+ *
+ * Conventions
+ *  - Every function returns DARIC_OK (0) or a non-zero status; the message of
+ *    the last failure on the calling thread is returned by daric_last_error().
+ *  - Tensors cross the boundary as `daric_tensor` views: a data pointer plus
+ *    sizes/strides in elements, the element size and the device ordinal.
+ *    No torch type appears in any signature.
+ *  - `stream` is a raw hipStream_t cast to uint64_t. 0 means the HIP null
+ *    stream; the Python layer resolves the reference's "0 = current torch
+ *    stream" rule (reference csrc/cache_ops/copier.cpp:27-30) before calling.
+ *  - All device work is asynchronous on `stream`. Nothing here synchronises,
+ *    except where a function says so.
+ *  - Host-side validation happens before any device work, so a failing call
+ *    leaves device memory untouched.
+ */
+#ifndef DARIC_CACHE_OPS_H
+#define DARIC_CACHE_OPS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DARIC_ABI_VERSION 1
+
+/* Status codes. */
+#define DARIC_OK 0
+#define DARIC_ERR_INVALID 1   /* argument validation failed (reference: TORCH_CHECK) */
+#define DARIC_ERR_RUNTIME 2   /* std::runtime_error in the reference (e.g. byte_size mismatch) */
+#define DARIC_ERR_HIP 3       /* a HIP runtime call failed */
+#define DARIC_ERR_NOMEM 4     /* host allocation failed */
+
+/* Element type codes carried by daric_tensor.dtype. */
+#define DARIC_DTYPE_UINT8 0
+#define DARIC_DTYPE_INT32 1
+#define DARIC_DTYPE_INT64 2
+#define DARIC_DTYPE_FLOAT16 3
+#define DARIC_DTYPE_BFLOAT16 4
+#define DARIC_DTYPE_FLOAT32 5
+#define DARIC_DTYPE_FP8_E4M3FN 6 /* OCP e4m3 (finite, NaN = 0x7F/0xFF); a uint8 cache is read as this */
+#define DARIC_DTYPE_OTHER 15
+
+#define DARIC_MAX_DIMS 8
+
+/* A strided tensor view. `data` is the address of element [0,...,0];
+ * `device` is the HIP device ordinal, or -1 for host memory. */
+typedef struct daric_tensor {
+    void* data;
+    int32_t ndim;
+    int32_t elem_size;
+    int32_t device;
+    int32_t dtype;
+    int64_t sizes[DARIC_MAX_DIMS];
+    int64_t strides[DARIC_MAX_DIMS];
+} daric_tensor;
+
+/* Rotary parameters for every re-rotation entry point.
+ *  inv_freq   : device fp32 array of rotary_dim/2 inverse frequencies; the
+ *               angle of pair i for a shift of d positions is the fp32 product
+ *               (float)d * inv_freq[i].
+ *  rotary_dim : number of rotated dims at the start of each K head row (even).
+ *  is_neox    : 1 pairs (i, i + rotary_dim/2); 0 pairs (2i, 2i+1) (GPT-J).
+ * Same meaning as vLLM RotaryEmbedding.rotary_dim / is_neox_style consumed at
+ * reference daric/adaption/adapter.py:176-194, 270-295, 378-396. */
+typedef struct daric_rope {
+    const float* inv_freq;
+    int32_t rotary_dim;
+    int32_t is_neox;
+} daric_rope;
+
+/* ---------------------------------------------------------------------- */
+/* Library                                                                 */
+/* ---------------------------------------------------------------------- */
+
+int daric_abi_version(void);
+const char* daric_last_error(void);
+
+/* Kernel timing: when enabled, every kernel launch of this library is
+ * bracketed by HIP events recorded on its launch stream. daric_timing_read
+ * synchronises those events and returns the summed kernel time (ms) and the
+ * number of launches since the last read (or enable), then resets them.
+ * This has no counterpart in the reference; it exists for measurement. */
+int daric_timing_enable(int enable);
+int daric_timing_read(double* total_ms, int64_t* launches);
+
+/* ---------------------------------------------------------------------- */
+/* CacheCopier: reference csrc/cache_ops/cache_ops.h:91-125, copier.cpp   */
+/* ---------------------------------------------------------------------- */
+
+typedef struct daric_copier daric_copier;
+
+/* CacheCopier.__init__ (reference bindings.cpp:10-11). */
+int daric_copier_create(daric_copier** out);
+int daric_copier_destroy(daric_copier* copier);
+
+/* CacheCopier.register_layer (reference copier.cpp:7-11): the tensor must be
+ * on a device; a second registration of `name` replaces the first. */
+int daric_copier_register_layer(daric_copier* copier, const char* name,
+                                const daric_tensor* tensor, int is_page_first);
+
+/* CacheCopier.register_store (reference copier.cpp:13-25): 1-D contiguous
+ * uint8 device buffer. Offsets of gather/scatter jobs are relative to it. */
+int daric_copier_register_store(daric_copier* copier, const daric_tensor* buffer);
+
+/* Per-layer fp32 K scales for an fp8 (e4m3) layer: `k_scale` is a device
+ * array of H floats (one per KV head). Without it an fp8 layer is rotated
+ * with scale 1, which is what the reference does (adapter.py:370-373).
+ * No counterpart in the reference (it has no scaled fp8 path). */
+int daric_copier_register_k_scale(daric_copier* copier, const char* name,
+                                  const daric_tensor* k_scale);
+
+/* CacheCopier.gather_pages (reference copier.cpp:41-76, kernels.cu:52-84,
+ * 127-217): for job i, copy the selected pages of layer `layer_names[i]` into
+ * the store at offsets[i], laid out [prefix][n_sel][page span bytes]. Pages
+ * whose block id is 0 are skipped and their store bytes left untouched.
+ * `indices_flat` is a 1-D contiguous int32 device tensor; job i uses
+ * indices_flat[indices_offsets[i] : indices_offsets[i+1]]. The n_* arguments
+ * are the lengths of the arrays that follow the reference's Python lists
+ * (offsets, byte_sizes, indices_offsets); mismatches are reported in the
+ * reference's order (helpers.cu:156-158). */
+int daric_copier_gather_pages(daric_copier* copier, const char* const* layer_names,
+                              int64_t n_jobs, const int64_t* offsets, int64_t n_offsets,
+                              const int64_t* byte_sizes, int64_t n_byte_sizes,
+                              const daric_tensor* indices_flat,
+                              const int64_t* indices_offsets,
+                              int64_t n_indices_offsets, uint64_t stream);
+
+/* CacheCopier.scatter_pages (reference copier.cpp:78-111, kernels.cu:86-123,
+ * 219-292): inverse of gather_pages, block id 0 skipped. */
+int daric_copier_scatter_pages(daric_copier* copier, const char* const* layer_names,
+                               int64_t n_jobs, const int64_t* offsets, int64_t n_offsets,
+                               const int64_t* byte_sizes, int64_t n_byte_sizes,
+                               const daric_tensor* indices_flat,
+                               const int64_t* indices_offsets,
+                               int64_t n_indices_offsets, uint64_t stream);
+
+/* Fused load path: scatter_pages plus the re-rotation the reference applies
+ * afterwards in the worker (adapter.py:196-295), in one pass over the bytes.
+ * Job i rotates the K rows of its first num_tokens[i] tokens (token j is slot
+ * j % PS of page j / PS of the job) by deltas[i] positions; V rows, rotary
+ * tails and tokens >= num_tokens[i] are copied unchanged. For an fp8 layer
+ * the K values are dequantised with the registered per-head scale, rotated
+ * in fp32 and requantised (saturating round-to-nearest-even).
+ * New entry point; no counterpart in the reference (which scatters in the
+ * store process and rotates later in the worker process). */
+int daric_copier_scatter_pages_rerotate(daric_copier* copier,
+                                        const char* const* layer_names, int64_t n_jobs,
+                                        const int64_t* offsets, int64_t n_offsets,
+                                        const int64_t* byte_sizes, int64_t n_byte_sizes,
+                                        const daric_tensor* indices_flat,
+                                        const int64_t* indices_offsets,
+                                        int64_t n_indices_offsets,
+                                        const int64_t* deltas, const int64_t* num_tokens,
+                                        const daric_rope* rope, uint64_t stream);
+
+/* batched_memcpy_d2h / batched_memcpy_h2d (reference helpers.cu:187-248):
+ * one hipMemcpyAsync per region on `stream`. */
+int daric_batched_memcpy_d2h(const daric_tensor* staging, const daric_tensor* shm,
+                             const int64_t* stg_offsets, const int64_t* shm_offsets,
+                             const int64_t* sizes, int64_t n, uint64_t stream);
+int daric_batched_memcpy_h2d(const daric_tensor* shm, const daric_tensor* staging,
+                             const int64_t* shm_offsets, const int64_t* stg_offsets,
+                             const int64_t* sizes, int64_t n, uint64_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* In-place re-rotation: replaces _fused_rerotate_kernel and               */
+/* Adapter._launch_triton_rerotate (reference adapter.py:30-88, 297-396).  */
+/* ---------------------------------------------------------------------- */
+
+/* A run of consecutive tokens that move by the same number of positions.
+ * Token j of the run (0 <= j < n_tokens) is position p = tok_start + j of the
+ * block list block_table[bt_offset ...]; its slot is
+ * block_table[bt_offset + p / PS] * PS + p % PS (reference adapter.py:164-170,
+ * 258-264). */
+typedef struct daric_rope_segment {
+    int64_t bt_offset;
+    int64_t tok_start;
+    int64_t n_tokens;
+    int64_t delta;
+} daric_rope_segment;
+
+/* Rotate, in place, the K rows of every listed token in every layer of
+ * `layers` (all with the same shape, strides and dtype; page_first as in
+ * reference adapter.py:311-368). `k_scales` is NULL or an [n_layers, H] fp32
+ * device tensor of per-head scales for fp8 layers. `block_table` is a 1-D
+ * contiguous int32 device tensor. */
+int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers, int page_first,
+                         const daric_tensor* block_table,
+                         const daric_rope_segment* segments, int64_t n_segments,
+                         const daric_rope* rope, const daric_tensor* k_scales,
+                         uint64_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Recompute selection (no reference kernel; the reference's budget is     */
+/* the positional DARICPolicy, daric/adaption/policy.py:45-103).           */
+/* ---------------------------------------------------------------------- */
+
+/* A chunk of consecutive tokens of one request: token j (0 <= j < n_tokens)
+ * lives at slot block_table[bt_offset + j / PS] * PS + j % PS of the paged
+ * cache and at row row_offset + j of the contiguous recomputed tensors.
+ * `k` is the number of tokens to select in it. */
+typedef struct daric_chunk {
+    int64_t bt_offset;
+    int64_t row_offset;
+    int64_t n_tokens;
+    int64_t k;
+} daric_chunk;
+
+/* keys[l, row_offset + j] = sum over (h, d) of (k_new[l, row, h, d] - K_cache)^2
+ * in fp32, in the fixed order documented in daric_amd/csrc/select.hip.
+ * layers: n_layers paged caches (same geometry); k_new: [n_layers, T, H, D]
+ * contiguous, same dtype; keys: [n_layers, T] fp32 contiguous. */
+int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_first,
+                       const daric_tensor* block_table, const daric_tensor* k_new,
+                       const daric_chunk* chunks, int64_t n_chunks,
+                       daric_tensor* keys, uint64_t stream);
+
+/* For every (layer, chunk) select the chunk's k tokens with the largest keys
+ * (ties: lower token index first) and write their chunk-local token indices
+ * in ascending order to out_idx[l, c, 0:k]; slots k..kmax-1 are set to -1.
+ * keys: [n_layers, T] fp32; out_idx: [n_layers, n_chunks, kmax] int32. */
+int daric_topk_per_chunk(const daric_tensor* keys, const daric_chunk* chunks,
+                         int64_t n_chunks, daric_tensor* out_idx, uint64_t stream);
+
+/* Write the selected rows of k_new / v_new ([n_layers, T, H, D]) into the K
+ * and V rows of their slots in the paged caches. sel_idx is the output of
+ * daric_topk_per_chunk (entries < 0 are ignored); slots in block 0 are
+ * skipped like the reference's copy kernels skip block 0. */
+int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_first,
+                     const daric_tensor* block_table, const daric_tensor* k_new,
+                     const daric_tensor* v_new, const daric_chunk* chunks,
+                     int64_t n_chunks, const daric_tensor* sel_idx, uint64_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DARIC_CACHE_OPS_H */

@@ -1,0 +1,140 @@
+"""CacheCopier gather/scatter byte semantics (CPU restatement).
+
+Follows reference csrc/cache_ops/copier.cpp:7-111 (registration, check order)
+and csrc/cache_ops/kernels.cu (index math of the copy kernels, :7-123, and the
+byte-size check of the launchers, :127-292):
+
+  gather : store[off + (p*n_sel + s)*span + b] = layer[p*prefix_stride + idx[s]*page_stride + b]
+  scatter: layer[p*prefix_stride + idx[s]*page_stride + b] = store[off + (p*n_sel + s)*span + b]
+
+for prefix index p, selected page s, byte b < span; pages with idx[s] == 0
+(vLLM's null block) are neither read nor written (kernels.cu:26,39,69,79,104,117).
+
+One deliberate difference: a block id outside [0, num_pages) is skipped like
+block 0. The reference reads/writes out of bounds there (undefined behaviour);
+the HIP kernels skip such pages instead of faulting, and so does this oracle.
+
+Layers are CPU torch tensors of any strides; byte offsets are taken from the
+address of element [0,...,0], as the reference takes them from data_ptr().
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import rope
+from .layout import (OracleError, _check, page_copy_shape, validate_common_job_inputs,
+                     validate_store_ranges)
+
+
+def byte_view(t: torch.Tensor):
+    """(uint8 view of t's whole storage, byte offset of element [0,...,0])."""
+    u8 = torch.empty(0, dtype=torch.uint8)
+    u8.set_(t.untyped_storage())
+    return u8, t.storage_offset() * t.element_size()
+
+
+class OracleCopier:
+    def __init__(self):
+        self.layers = {}
+        self.store = None
+        self.k_scales = {}
+
+    def register_layer(self, name, tensor: torch.Tensor, is_page_first: bool):
+        self.layers[name] = (tensor, bool(is_page_first))
+
+    def register_store(self, buffer: torch.Tensor):
+        _check(buffer.dim() == 1, "store buffer must be 1D")
+        _check(buffer.dtype == torch.uint8, "store buffer must be uint8")
+        _check(buffer.is_contiguous(), "store buffer must be contiguous")
+        self.store = buffer
+
+    def register_k_scale(self, name, k_scale):
+        self.k_scales[name] = np.asarray(k_scale, dtype=np.float64)
+
+    # ------------------------------------------------------------------ #
+    def _plan(self, layer_names, offsets, byte_sizes, indices_flat, indices_offsets):
+        """Check order of copier.cpp:46-66 and the launcher's byte-size check."""
+        _check(self.store is not None, "store buffer not registered; call register_store() first")
+        n = len(layer_names)
+        if n == 0:
+            return None
+        idx = torch.as_tensor(indices_flat)
+        validate_common_job_inputs(n, list(offsets), list(byte_sizes), list(indices_offsets),
+                                   idx.numel(), (True, idx.dim() == 1, idx.dtype == torch.int32,
+                                                 idx.is_contiguous()))
+        validate_store_ranges(list(offsets), list(byte_sizes), self.store.numel())
+        jobs = []
+        for name in layer_names:
+            _check(name in self.layers, "layer not registered: ", name)
+        for i, name in enumerate(layer_names):
+            t, pf = self.layers[name]
+            shp = page_copy_shape(tuple(t.shape), tuple(t.stride()), t.element_size(), pf)
+            n_sel = int(indices_offsets[i + 1] - indices_offsets[i])
+            num = shp.prefix_size * n_sel * shp.suffix_size
+            if int(byte_sizes[i]) != num:
+                raise OracleError(
+                    f"byte_size mismatch at job {i} | C++ expected bytes: {num} | "
+                    f"Python passed bytes: {int(byte_sizes[i])} | Tensor shape: "
+                    f"[{', '.join(str(x) for x in t.shape)}] | Tensor strides: "
+                    f"[{', '.join(str(x) for x in t.stride())}]")
+            sel = idx[int(indices_offsets[i]): int(indices_offsets[i + 1])].tolist()
+            jobs.append((name, t, pf, shp, int(offsets[i]), sel))
+        return jobs
+
+    @staticmethod
+    def _pages(shp, sel):
+        for p in range(shp.prefix_size):
+            for s, page in enumerate(sel):
+                if page <= 0 or page >= shp.num_pages:
+                    continue
+                yield p, s, page
+
+    def gather_pages(self, layer_names, offsets, byte_sizes, indices_flat, indices_offsets):
+        jobs = self._plan(layer_names, offsets, byte_sizes, indices_flat, indices_offsets)
+        if not jobs:
+            return
+        for name, t, pf, shp, off, sel in jobs:
+            mem, base = byte_view(t)
+            span, n_sel = shp.suffix_size, len(sel)
+            for p, s, page in self._pages(shp, sel):
+                src = base + p * shp.prefix_stride + page * shp.page_stride
+                dst = off + (p * n_sel + s) * span
+                self.store[dst: dst + span] = mem[src: src + span]
+
+    def scatter_pages(self, layer_names, offsets, byte_sizes, indices_flat, indices_offsets):
+        jobs = self._plan(layer_names, offsets, byte_sizes, indices_flat, indices_offsets)
+        if not jobs:
+            return
+        for name, t, pf, shp, off, sel in jobs:
+            mem, base = byte_view(t)
+            span, n_sel = shp.suffix_size, len(sel)
+            for p, s, page in self._pages(shp, sel):
+                dst = base + p * shp.prefix_stride + page * shp.page_stride
+                src = off + (p * n_sel + s) * span
+                mem[dst: dst + span] = self.store[src: src + span]
+
+    def scatter_pages_rerotate(self, layer_names, offsets, byte_sizes, indices_flat,
+                               indices_offsets, deltas, num_tokens, inv_freq, rotary_dim,
+                               is_neox):
+        """scatter_pages, then the K rows of the first num_tokens[i] tokens of
+        job i are rotated by deltas[i] (token j = slot j % PS of page j // PS of
+        the job, pages with block id 0 or out of range excluded), i.e. the
+        reference's scatter (gpu_kv_io.py:569-572) followed by its worker-side
+        apply_rerotate_load (adapter.py:196-295) restricted to the loaded pages."""
+        jobs = self._plan(layer_names, offsets, byte_sizes, indices_flat, indices_offsets)
+        if not jobs:
+            return
+        self.scatter_pages(layer_names, offsets, byte_sizes, indices_flat, indices_offsets)
+        for i, (name, t, pf, shp, off, sel) in enumerate(jobs):
+            d, nt = int(deltas[i]), int(num_tokens[i])
+            if d == 0 or nt <= 0:
+                continue
+            ps = rope.k_view(t, pf, rotary_dim).shape[1]
+            slots = []
+            for j in range(min(nt, len(sel) * ps)):
+                page = sel[j // ps]
+                if 0 < page < shp.num_pages:
+                    slots.append(page * ps + j % ps)
+            rope.rotate_slots(t, pf, slots, d, inv_freq, rotary_dim, is_neox,
+                              self.k_scales.get(name))

@@ -1,0 +1,151 @@
+"""Recompute selection: deviation keys, per-chunk top-k, merge (CPU restatement).
+
+The reference has no such kernels: its "distribution-aware recomputation" is the
+positional DARICPolicy (reference daric/adaption/policy.py:45-103) and the merge
+is vLLM's own reshape_and_cache writing recomputed rows into the same slots
+(daric/integration/vllm/worker.py:336-345, utils.py:406-427). The spec followed
+here is the selection workload of the task's configuration 3:
+
+  key[l, t] = sum over (h, d) of (K_new[l, t, h, d] - K_cache[l, slot(t), h, d])^2
+
+in float32, in this fixed order (the HIP kernel sums in exactly this order, so
+the keys and therefore the selected indices are bit-exact):
+  - the token's H*D elements are taken in (h, d) order and cut into vectors of
+    VEC = 8 consecutive elements; vector v belongs to lane v % 64 of a 64-lane
+    wavefront and is visited in round v // 64;
+  - each lane accumulates acc = acc + diff*diff element by element (each
+    operation rounded to float32, no fused multiply-add), rounds ascending,
+    elements of a vector ascending;
+  - the 64 lane sums are combined by a butterfly: for off in 32,16,8,4,2,1:
+    acc[l] = acc[l] + acc[l ^ off]; the key is acc[0].
+Cached fp8 values are dequantised as float32(code value * k_scale[h]).
+Keys are ranked by their float32 bit pattern as an unsigned integer (keys are
+>= +0; any NaN is stored as 0x7FC00000 and ranks above +inf). Ties go to the
+lower token index. The k selected chunk-local indices are returned ascending.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import fp8
+from .layout import rope_geometry
+
+VEC = 8
+LANES = 64
+NAN_KEY = np.uint32(0x7FC00000)
+
+
+def v_view(layer: torch.Tensor, page_first: bool) -> torch.Tensor | None:
+    """[num_blocks, PS, H, D] view of the V head rows (None for a 3-D MLA cache)."""
+    nd = layer.dim()
+    if nd == 5:
+        return layer[:, 1] if page_first else layer[1]
+    if nd == 4:
+        d = layer.shape[3] // 2
+        return layer.permute(0, 2, 1, 3)[..., d:]
+    return None
+
+
+def k_rows_view(layer: torch.Tensor, page_first: bool) -> torch.Tensor:
+    """[num_blocks, PS, H, D] view of the full K head rows."""
+    nd = layer.dim()
+    if nd == 5:
+        return layer[:, 0] if page_first else layer[0]
+    if nd == 4:
+        d = layer.shape[3] // 2
+        return layer.permute(0, 2, 1, 3)[..., :d]
+    return layer.unsqueeze(2)
+
+
+def _as_f32(x: torch.Tensor, k_scale=None) -> np.ndarray:
+    if x.dtype == torch.uint8:
+        v = fp8.decode(x.numpy()).astype(np.float32)
+        s = np.ones(x.shape[-2], np.float32) if k_scale is None else np.asarray(k_scale, np.float32)
+        return (v * s[:, None]).astype(np.float32)
+    return x.to(torch.float32).numpy()
+
+
+def fixed_order_sumsq(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Keys of rows a, b: [T, N] float32 -> [T] float32, in the order above."""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    t, n = a.shape
+    d = (a - b).astype(np.float32)
+    sq = (d * d).astype(np.float32)
+    n_vec = -(-n // VEC)
+    rounds = -(-n_vec // LANES)
+    padded = np.zeros((t, rounds * LANES * VEC), np.float32)
+    padded[:, :n] = sq
+    padded = padded.reshape(t, rounds, LANES, VEC)
+    acc = np.zeros((t, LANES), np.float32)
+    for r in range(rounds):
+        for i in range(VEC):
+            acc = (acc + padded[:, r, :, i]).astype(np.float32)
+    lanes = np.arange(LANES)
+    for off in (32, 16, 8, 4, 2, 1):
+        acc = (acc + acc[:, lanes ^ off]).astype(np.float32)
+    key = acc[:, 0].copy()
+    key[np.isnan(key)] = NAN_KEY.view(np.float32)
+    return key
+
+
+def chunk_slots(block_table, bt_offset, n_tokens, page_size):
+    bt = np.asarray(block_table)
+    j = np.arange(n_tokens)
+    return bt[bt_offset + j // page_size].astype(np.int64), j % page_size
+
+
+def deviation(layers, page_first, block_table, k_new, chunks, k_scales=None) -> np.ndarray:
+    """keys [L, T] for chunks (bt_offset, row_offset, n_tokens, k); rows of T
+    not covered by any chunk are left 0."""
+    L, T = len(layers), k_new.shape[1]
+    keys = np.zeros((L, T), np.float32)
+    for l, layer in enumerate(layers):
+        kv = k_rows_view(layer, page_first)
+        ps, h, d = kv.shape[1], kv.shape[2], kv.shape[3]
+        ks = None if k_scales is None else k_scales[l]
+        for bt_offset, row_offset, n_tokens, _k in chunks:
+            blk, s = chunk_slots(block_table, bt_offset, n_tokens, ps)
+            cached = _as_f32(kv[torch.as_tensor(blk), torch.as_tensor(s)], ks).reshape(n_tokens, h * d)
+            new = k_new[l, row_offset: row_offset + n_tokens].to(torch.float32).numpy().reshape(n_tokens, h * d)
+            keys[l, row_offset: row_offset + n_tokens] = fixed_order_sumsq(new, cached)
+    return keys
+
+
+def topk_chunk(keys: np.ndarray, k: int) -> np.ndarray:
+    """Indices of the k largest keys (by uint32 bit pattern), ties to the lower
+    index, returned ascending. Uses numpy's stable lexsort."""
+    bits = np.asarray(keys, np.float32).view(np.uint32).astype(np.int64)
+    order = np.lexsort((np.arange(len(bits)), -bits))
+    return np.sort(order[: min(k, len(bits))])
+
+
+def topk_per_chunk(keys: np.ndarray, chunks, kmax: int) -> np.ndarray:
+    L = keys.shape[0]
+    out = np.full((L, len(chunks), kmax), -1, np.int32)
+    for l in range(L):
+        for c, (_bt, row_offset, n_tokens, k) in enumerate(chunks):
+            sel = topk_chunk(keys[l, row_offset: row_offset + n_tokens], int(k))
+            out[l, c, : len(sel)] = sel
+    return out
+
+
+def merge_rows(layers, page_first, block_table, k_new, v_new, chunks, sel_idx) -> None:
+    """Write selected K/V rows into their slots (block 0 / out of range skipped)."""
+    for l, layer in enumerate(layers):
+        kv = k_rows_view(layer, page_first)
+        vv = v_view(layer, page_first)
+        nb, ps = kv.shape[0], kv.shape[1]
+        for c, (bt_offset, row_offset, n_tokens, _k) in enumerate(chunks):
+            for j in sel_idx[l, c]:
+                j = int(j)
+                if j < 0 or j >= n_tokens:
+                    continue
+                blk = int(np.asarray(block_table)[bt_offset + j // ps])
+                s = j % ps
+                if blk <= 0 or blk >= nb:
+                    continue
+                kv[blk, s].copy_(k_new[l, row_offset + j].view(kv.dtype))
+                if vv is not None:
+                    vv[blk, s].copy_(v_new[l, row_offset + j].view(vv.dtype))

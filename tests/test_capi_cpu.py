@@ -1,0 +1,252 @@
+"""CPU-side checks of the C-ABI library (no GPU needed, no kernel launched).
+
+- the built library loads and exports every function include/daric_cache_ops.h
+  declares;
+- host validation rejects bad jobs with the same message, in the same order,
+  as the oracle's restatement of the reference's checks (descriptors carry fake
+  device pointers; every case fails before any HIP call);
+- the element conversions and the fast divider used by the kernels, compiled
+  for the host from the same headers, agree with torch / exact division.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from daric_amd import _lib
+from oracle import fp8 as ofp8
+from oracle.copy import OracleCopier
+from oracle.layout import OracleError
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "daric_cache_ops.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from daric_amd import build
+        build.build(verbose=False)
+    return _lib.load()
+
+
+@pytest.fixture(scope="module")
+def hosttest(lib):
+    from daric_amd import build
+    h = ctypes.CDLL(build.HOSTTEST_LIB)
+    h.daric_hosttest_encode_e4m3.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+    h.daric_hosttest_encode_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+    h.daric_hosttest_e4m3_to_f32.argtypes = [ctypes.c_uint32]
+    h.daric_hosttest_e4m3_to_f32.restype = ctypes.c_float
+    h.daric_hosttest_f32_to_f16.argtypes = [ctypes.c_float]
+    h.daric_hosttest_f32_to_f16.restype = ctypes.c_uint32
+    h.daric_hosttest_fastdiv_errors.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+    h.daric_hosttest_fastdiv_errors.restype = ctypes.c_int64
+    return h
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(daric_\w+)\s*\(", text, re.M)))
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 18
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover the header"
+    assert lib.daric_abi_version() == 1
+
+
+def fake(shape, dtype, device=0, strides=None, ptr=0x10000000):
+    t = torch.empty(0, dtype=dtype)
+    d = _lib.DaricTensor()
+    d.data = ptr
+    d.ndim = len(shape)
+    d.elem_size = t.element_size()
+    d.device = device
+    d.dtype = _lib.DTYPE_CODES[dtype]
+    if strides is None:
+        strides, acc = [], 1
+        for s in reversed(shape):
+            strides.insert(0, acc)
+            acc *= s
+    for i, (s, st) in enumerate(zip(shape, strides)):
+        d.sizes[i] = s
+        d.strides[i] = st
+    return d
+
+
+class CCopier:
+    """Direct ctypes driver of the C copier (the Python shim needs real tensors)."""
+
+    def __init__(self, lib):
+        self.lib = lib
+        self.h = ctypes.c_void_p()
+        assert lib.daric_copier_create(ctypes.byref(self.h)) == 0
+
+    def err(self, status):
+        return None if status == 0 else self.lib.daric_last_error().decode()
+
+    def register_layer(self, name, d, pf):
+        return self.err(self.lib.daric_copier_register_layer(self.h, name.encode(), ctypes.byref(d), pf))
+
+    def register_store(self, d):
+        return self.err(self.lib.daric_copier_register_store(self.h, ctypes.byref(d)))
+
+    def gather(self, names, offsets, sizes, idx, idx_off):
+        return self.err(self.lib.daric_copier_gather_pages(
+            self.h, _lib.str_array(names), len(names), _lib.i64_array(offsets), len(offsets),
+            _lib.i64_array(sizes), len(sizes), ctypes.byref(idx), _lib.i64_array(idx_off),
+            len(idx_off), ctypes.c_uint64(0)))
+
+
+def oracle_error(fn):
+    try:
+        fn()
+    except OracleError as e:
+        return str(e)
+    return None
+
+
+LAYER_SHAPE = (2, 4, 2, 2, 4)
+
+
+def test_validation_matches_oracle(lib):
+    c = CCopier(lib)
+    o = OracleCopier()
+    layer = torch.zeros(LAYER_SHAPE, dtype=torch.float16)
+    assert c.register_layer("a", fake(LAYER_SHAPE, torch.float16), 0) is None
+    o.register_layer("a", layer, False)
+    idx = fake((1,), torch.int32, ptr=0x20000000)
+    oidx = torch.tensor([1], dtype=torch.int32)
+
+    def both(names, offs, sizes, idx_off, i=idx, oi=oidx):
+        return c.gather(names, offs, sizes, i, idx_off), oracle_error(
+            lambda: o.gather_pages(names, offs, sizes, oi, idx_off))
+
+    e_c, e_o = both(["a"], [0], [64], [0, 1])
+    assert e_c == e_o and "store buffer not registered" in e_c
+    assert c.register_store(fake((128,), torch.uint8, ptr=0x30000000)) is None
+    o.register_store(torch.zeros(128, dtype=torch.uint8))
+    assert both([], [], [], [0]) == (None, None)
+    cases = [
+        (["a"], [], [64], [0, 1]),
+        (["a"], [0], [64, 1], [0, 1]),
+        (["a"], [0], [64], [0]),
+        (["a"], [0], [64], [0, 2]),
+        (["a", "a"], [0, 0], [0, 0], [1, 0, 1]),
+        (["a"], [-1], [64], [0, 1]),
+        (["a"], [100], [64], [0, 1]),
+        (["a"], [200], [0], [0, 1]),
+        (["b"], [0], [64], [0, 1]),
+        (["a"], [0], [63], [0, 1]),
+    ]
+    for case in cases:
+        e_c, e_o = both(*case)
+        assert e_c is not None and e_c == e_o, (case, e_c, e_o)
+    # indices tensor properties
+    e_c = c.gather(["a"], [0], [64], fake((1,), torch.int64, ptr=0x20000000), [0, 1])
+    assert e_c == "indices_flat must be int32"
+    e_c = c.gather(["a"], [0], [64], fake((1,), torch.int32, device=-1), [0, 1])
+    assert e_c == "indices_flat must be on CUDA"
+    e_c = c.gather(["a"], [0], [64], fake((1,), torch.int32, device=1), [0, 1])
+    assert e_c == "indices_flat must be on the same device as kvcache"
+
+
+def test_layout_errors_match_oracle(lib):
+    from oracle.layout import page_copy_shape
+    cases = [
+        ((2, 5, 16, 4, 32), (5 * 16 * 4 * 64, 16 * 4 * 64, 4 * 64, 64, 1), False),   # hole
+        ((2, 5, 16, 4, 32), (5 * 16 * 32, 16 * 32, 32, 0, 1), False),                # stride 0
+        ((2, 5, 16, 4, 32), (0, 16 * 4 * 32, 4 * 32, 32, 1), False),                 # K/V overlap
+        ((5, 2, 16, 4, 32), (16 * 4 * 32, 16 * 4 * 32, 4 * 32, 32, 1), True),        # pages overlap
+    ]
+    for shape, strides, pf in cases:
+        c = CCopier(lib)
+        assert c.register_layer("x", fake(shape, torch.float16, strides=strides), int(pf)) is None
+        assert c.register_store(fake((1 << 20,), torch.uint8, ptr=0x30000000)) is None
+        e_c = c.gather(["x"], [0], [64], fake((1,), torch.int32, ptr=0x20000000), [0, 1])
+        e_o = oracle_error(lambda: page_copy_shape(shape, strides, 2, pf))
+        assert e_o is not None and e_c == e_o, (shape, e_c, e_o)
+
+
+def test_register_errors(lib):
+    c = CCopier(lib)
+    assert c.register_layer("a", fake(LAYER_SHAPE, torch.float16, device=-1), 0) == \
+        "kvcache tensor must be on GPU: a"
+    assert c.register_store(fake((4, 4), torch.uint8)) == "store buffer must be 1D"
+    assert c.register_store(fake((16,), torch.int32)) == "store buffer must be uint8"
+    assert c.register_store(fake((16,), torch.uint8, device=-1)) == "staging buffer must be on CUDA"
+    assert c.register_store(fake((16,), torch.uint8, strides=(2,))) == "store buffer must be contiguous"
+
+
+def test_rerotate_layout_errors(lib):
+    rope = _lib.DaricRope()
+    rope.inv_freq = 0x40000000
+    rope.rotary_dim = 16
+    rope.is_neox = 1
+    bt = fake((4,), torch.int32, ptr=0x20000000)
+    seg = (_lib.DaricRopeSegment * 1)(_lib.DaricRopeSegment(0, 0, 16, 5))
+
+    def run(shape, pf, dtype=torch.bfloat16, rd=16, nseg_tokens=16):
+        rope.rotary_dim = rd
+        seg[0].n_tokens = nseg_tokens
+        arr = (_lib.DaricTensor * 1)(fake(shape, dtype))
+        st = lib.daric_rerotate_pages(arr, 1, pf, ctypes.byref(bt), seg, 1, ctypes.byref(rope), None,
+                                      ctypes.c_uint64(0))
+        return lib.daric_last_error().decode() if st else None
+
+    assert "page_first must be true" in run((8, 2, 4, 32), 0)
+    assert "rotary_dim must be positive, even, and no greater" in run((8, 2, 4, 32), 1, rd=32)
+    assert "Unsupported KV cache rank for rerotate: 2" in run((8, 32), 1)
+    assert "unsupported KV cache dtype" in run((2, 8, 4, 2, 16), 0, dtype=torch.float32)
+    assert "reads past the end of block_table" in run((2, 8, 4, 2, 16), 0, nseg_tokens=17)
+
+
+def test_host_fp8_conversion_matches_oracle(hosttest):
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * np.float32(50),
+        rng.standard_normal(50000).astype(np.float32) * np.float32(1e-2),
+        (rng.random(50000).astype(np.float32) * 600 - 300),
+        np.array([0.0, -0.0, 448, 449, 463.99, 464, 464.01, 1e9, -1e9, np.inf, -np.inf,
+                  2 ** -9, 2 ** -10, 3 * 2 ** -11, 2 ** -6, 2 ** -6 * 0.999], np.float32),
+    ]).astype(np.float32)
+    # every midpoint between adjacent e4m3 values (rounding ties)
+    pos = np.unique(ofp8.decode(np.arange(0x7f)))
+    mids = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
+    vals = np.concatenate([vals, mids, -mids]).astype(np.float32)
+    out = np.empty(vals.shape, np.uint8)
+    hosttest.daric_hosttest_encode_e4m3(vals.ctypes.data, out.ctypes.data, len(vals))
+    want = ofp8.encode(vals)
+    assert np.array_equal(out, want)
+    for c in range(256):
+        got = hosttest.daric_hosttest_e4m3_to_f32(c)
+        ref = float(ofp8.decode([c])[0])
+        assert (np.isnan(got) and np.isnan(ref)) or got == ref
+
+
+def test_host_bf16_f16_conversion_matches_torch(hosttest):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2 ** 32, 400000, dtype=np.uint64).astype(np.uint32)
+    vals = bits.view(np.float32)
+    vals = vals[~np.isnan(vals)]
+    out = np.empty(vals.shape, np.uint16)
+    hosttest.daric_hosttest_encode_bf16(vals.ctypes.data, out.ctypes.data, len(vals))
+    want = torch.from_numpy(vals.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(out, want)
+    sample = rng.standard_normal(2000).astype(np.float32) * 1e3
+    got = np.array([hosttest.daric_hosttest_f32_to_f16(float(v)) for v in sample], np.uint16)
+    want = torch.from_numpy(sample).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("d", [1, 2, 3, 7, 8, 16, 68, 100, 128, 1000, 65535, 2 ** 20 + 7])
+def test_host_fastdiv(hosttest, d):
+    assert hosttest.daric_hosttest_fastdiv_errors(d, 0, 1 << 20) == 0
+    assert hosttest.daric_hosttest_fastdiv_errors(d, (1 << 31) - (1 << 18), 1 << 31) == 0

@@ -1,0 +1,94 @@
+"""Pins the CPU oracle's deviation keys, top-k and merge.
+
+Independent facts: the fixed-order float32 sum agrees with a float64 sum to
+float32 accuracy and with a scalar float32 walk in the documented order on tiny
+rows (brute force); top-k agrees with Python's stable sorted() on (-key, index);
+merge lands rows where torch indexing says.
+"""
+import numpy as np
+import torch
+
+from oracle import select
+
+
+def scalar_walk(a, b):
+    """Brute force in np.float32 scalars, following the documented order."""
+    n = len(a)
+    acc = [np.float32(0)] * 64
+    v = 0
+    while v * 8 < n:
+        lane = v % 64
+        for i in range(8):
+            e = v * 8 + i
+            if e < n:
+                d = np.float32(np.float32(a[e]) - np.float32(b[e]))
+                acc[lane] = np.float32(acc[lane] + np.float32(d * d))
+        v += 1
+    for off in (32, 16, 8, 4, 2, 1):
+        acc = [np.float32(acc[l] + acc[l ^ off]) for l in range(64)]
+    return acc[0]
+
+
+def test_sumsq_matches_float64_and_scalar_walk():
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((6, 1024)).astype(np.float32)
+    b = (a + 0.1 * rng.standard_t(3, size=a.shape)).astype(np.float32)
+    k = select.fixed_order_sumsq(a, b)
+    ref = ((a.astype(np.float64) - b.astype(np.float64)) ** 2).sum(1)
+    assert np.all(np.abs(k - ref) <= 1e-5 * ref)
+    for n in (8, 40, 130, 600):
+        x = rng.standard_normal((1, n)).astype(np.float32) * np.float32(1e3) ** rng.integers(-2, 3, n)
+        y = rng.standard_normal((1, n)).astype(np.float32)
+        assert select.fixed_order_sumsq(x.astype(np.float32), y)[0] == scalar_walk(x[0], y[0])
+
+
+def test_sumsq_exact_counts_and_nan():
+    a = np.ones((2, 1024), np.float32)
+    b = np.zeros((2, 1024), np.float32)
+    b[1, 5] = np.inf
+    a[1, 5] = np.inf
+    k = select.fixed_order_sumsq(a, b)
+    assert k[0] == 1024.0
+    assert k.view(np.uint32)[1] == 0x7FC00000
+
+
+def test_topk_matches_stable_sort():
+    rng = np.random.default_rng(1)
+    for n, k in ((512, 77), (2048, 205), (37, 5), (10, 10), (5, 9)):
+        keys = rng.integers(0, 6, n).astype(np.float32)  # heavy ties
+        keys[rng.integers(0, n)] = np.inf
+        want = sorted(sorted(range(n), key=lambda i: (-keys[i], i))[:k])
+        assert select.topk_chunk(keys, k).tolist() == want
+    keys = np.array([1.0, 3.0, 3.0, 2.0, 3.0], np.float32)
+    assert select.topk_chunk(keys, 2).tolist() == [1, 2]
+    nan = np.array([0x7FC00000], np.uint32).view(np.float32)[0]
+    keys = np.array([np.inf, nan, 5.0], np.float32)
+    assert select.topk_chunk(keys, 1).tolist() == [1]
+
+
+def test_merge_rows_land_in_slots():
+    nb, ps, h, d = 6, 4, 2, 8
+    layer = torch.zeros(2, nb, ps, h, d, dtype=torch.bfloat16)
+    k_new = torch.randn(1, 10, h, d).to(torch.bfloat16)
+    v_new = torch.randn(1, 10, h, d).to(torch.bfloat16)
+    bt = np.array([3, 0, 5], np.int32)
+    chunks = [(0, 0, 10, 3)]
+    sel = np.array([[[1, 4, 9]]], np.int32)
+    select.merge_rows([layer], False, bt, k_new, v_new, chunks, sel)
+    assert torch.equal(layer[0, 3, 1], k_new[0, 1]) and torch.equal(layer[1, 3, 1], v_new[0, 1])
+    assert torch.equal(layer[0, 5, 1], k_new[0, 9]) and torch.equal(layer[1, 5, 1], v_new[0, 9])
+    assert layer[:, 0].abs().sum() == 0  # token 4 maps to block 0: skipped
+    assert int((layer != 0).sum()) == 4 * h * d - int((k_new[0, [1, 9]] == 0).sum() + (v_new[0, [1, 9]] == 0).sum())
+
+
+def test_deviation_uses_slots():
+    g = torch.Generator().manual_seed(2)
+    nb, ps, h, d = 5, 4, 2, 8
+    layer = torch.randn(2, nb, ps, h, d, generator=g).to(torch.bfloat16)
+    bt = np.array([4, 1], np.int32)
+    k_new = torch.randn(1, 8, h, d, generator=g).to(torch.bfloat16)
+    keys = select.deviation([layer], False, bt, k_new, [(0, 0, 8, 2)])
+    for j in range(8):
+        cached = layer[0, bt[j // ps], j % ps].double()
+        ref = ((k_new[0, j].double() - cached) ** 2).sum().item()
+        assert abs(keys[0, j] - ref) <= 1e-5 * ref
