@@ -93,12 +93,22 @@ def rotate_slots(layer: torch.Tensor, page_first: bool, slots, delta: int,
     kv = k_view(layer, page_first, rotary_dim)
     ps, h = kv.shape[1], kv.shape[2]
     scale = np.ones(h) if k_scale is None else np.asarray(k_scale, dtype=np.float64)
-    for slot in slots:
-        blk, s = int(slot) // ps, int(slot) % ps
-        rows = kv[blk, s]                       # [H, D] view
-        vals = _to_values(rows.clone(), scale)
-        out = rotate_rows(vals, delta, inv_freq, rotary_dim, is_neox)
-        rows.copy_(_from_values(out, layer.dtype, scale))
+    slots = np.asarray(list(slots), dtype=np.int64)
+    if slots.size == 0:
+        return
+    if np.unique(slots).size != slots.size:
+        # a slot listed twice is rotated twice, one after the other
+        for slot in slots:
+            blk, s = int(slot) // ps, int(slot) % ps
+            rows = kv[blk, s]                   # [H, D] view
+            vals = _to_values(rows.clone(), scale)
+            out = rotate_rows(vals, delta, inv_freq, rotary_dim, is_neox)
+            rows.copy_(_from_values(out, layer.dtype, scale))
+        return
+    blk, s = torch.from_numpy(slots // ps), torch.from_numpy(slots % ps)
+    vals = _to_values(kv[blk, s], scale)        # [n, H, D]
+    out = rotate_rows(vals, delta, inv_freq, rotary_dim, is_neox)
+    kv[blk, s] = _from_values(out, layer.dtype, scale)
 
 
 def segment_slots(block_table, bt_offset: int, tok_start: int, n_tokens: int,
