@@ -85,6 +85,37 @@ def algorithmic_bytes(cfg, T=None, L=None):
     return T * L * 2 * (2 * cfg["kv_heads"] * cfg["head_dim"] * 2)
 
 
+def time_steps(step, steps, warmup, stream):
+    """W untimed warm-up steps, then two timed passes of `steps` steps each:
+    pass 1 (the measurement) brackets the K steps with device synchronisation
+    and HIP events on `stream`; pass 2 times every kernel launch of the library
+    with its own HIP events on the launch stream (kernel duration for the
+    roofline), kept out of pass 1 so that the per-launch events cannot slow the
+    measured steps."""
+    from daric_amd import cache_ops
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        step()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = start.elapsed_time(stop) / steps
+    cache_ops.timing_enable(True)
+    cache_ops.timing_read()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    kern_ms, launches = cache_ops.timing_read()
+    cache_ops.timing_enable(False)
+    return dict(step_ms=step_ms, wall_s=wall, kern_ms=kern_ms / max(launches, 1),
+                launches_per_step=launches / max(steps, 1))
+
+
 def run_gpu(cfg, steps, warmup):
     from daric_amd import cache_ops
     dev = torch.device("cuda:0")
@@ -102,23 +133,7 @@ def run_gpu(cfg, steps, warmup):
         cp.scatter_pages_rerotate(j["names"], j["offsets"], j["sizes"], idx, j["ioff"], j["deltas"],
                                   j["ntok"], inv, cfg["head_dim"], True, stream.cuda_stream)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    cache_ops.timing_enable(True)
-    cache_ops.timing_read()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(steps):
-        step()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kern_ms, launches = cache_ops.timing_read()
-    cache_ops.timing_enable(False)
-    step_ms = start.elapsed_time(stop) / steps
+    fused = time_steps(step, steps, warmup, stream)
 
     # return path: gather the whole request into [L, 2, T, H, D]
     T, L = w["T"], w["L"]
@@ -137,21 +152,9 @@ def run_gpu(cfg, steps, warmup):
     def gstep():
         gcp.gather_pages(w["names"], g_off, g_sizes, g_flat, g_ioff, stream.cuda_stream)
 
-    for _ in range(warmup):
-        gstep()
-    torch.cuda.synchronize()
-    cache_ops.timing_enable(True)
-    cache_ops.timing_read()
-    start.record(stream)
-    for _ in range(steps):
-        gstep()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    g_kern_ms, g_launches = cache_ops.timing_read()
-    cache_ops.timing_enable(False)
-    g_step_ms = start.elapsed_time(stop) / steps
-    return dict(step_ms=step_ms, wall_s=wall, kern_ms=kern_ms / max(launches, 1), launches=launches,
-                g_step_ms=g_step_ms, g_kern_ms=g_kern_ms / max(g_launches, 1), T=T, L=L)
+    gather = time_steps(gstep, steps, warmup, stream)
+    return dict(step_ms=fused["step_ms"], wall_s=fused["wall_s"], kern_ms=fused["kern_ms"],
+                g_step_ms=gather["step_ms"], g_kern_ms=gather["kern_ms"], T=T, L=L)
 
 
 def run_cpu_baseline(cfg, budget_s=12.0):
@@ -189,6 +192,19 @@ def run_cpu_baseline(cfg, budget_s=12.0):
                 GBps=algorithmic_bytes(cfg) / med / 1e9)
 
 
+def run_copy_calibration(steps, nbytes=1 << 30):
+    """A plain contiguous device copy of `nbytes` (reads nbytes, writes nbytes),
+    run `steps` times: the kernel whose rocprofv3 FETCH_SIZE / WRITE_SIZE
+    readings calibrate those counters against a known byte count."""
+    dev = torch.device("cuda:0")
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device=dev).fill_(7)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def read_traffic():
     """HBM bytes per launch of the fused kernel from the committed rocprofv3
     PMC summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration)."""
@@ -211,6 +227,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a plain 1 GiB device copy (torch copy_) `steps` times, the "
+                         "known-size reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -219,6 +238,8 @@ def main():
         sys.exit(2)
     cfg = CFG2
     r = run_gpu(cfg, a.steps, a.warmup)
+    if a.calib_copy:
+        run_copy_calibration(a.steps)
     nbytes = algorithmic_bytes(cfg)
     tok_s = r["T"] / (r["step_ms"] / 1e3)
     achieved = nbytes / (r["kern_ms"] / 1e3) / 1e9
@@ -243,7 +264,7 @@ def main():
         "GBps": nbytes / (r["step_ms"] / 1e3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBPS, "traffic": read_traffic(),
-                     "kernel": "scatter_rotate_kernel<bf16,neox>", "kernel_ms": r["kern_ms"],
+                     "kernel": "scatter_rotate_lane_kernel<bf16,neox>", "kernel_ms": r["kern_ms"],
                      "algorithmic_bytes": nbytes},
         "gather": {"ms_per_step": r["g_step_ms"], "kernel_ms": r["g_kern_ms"],
                    "GBps": g_achieved, "frac": g_achieved / PEAK_HBM_GBPS,

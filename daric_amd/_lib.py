@@ -6,6 +6,7 @@ device pointers and hipStream_t values from torch are then valid in it.
 """
 from __future__ import annotations
 
+import array
 import ctypes
 import os
 from ctypes import POINTER, c_char_p, c_double, c_int, c_int32, c_int64, c_uint64, c_void_p
@@ -54,7 +55,7 @@ class DaricChunk(ctypes.Structure):
 
 P = POINTER
 T = P(DaricTensor)
-I64P = P(c_int64)
+I64P = c_void_p  # address of an I64 buffer
 STRS = P(c_char_p)
 
 # name -> (restype, argtypes); mirrors include/daric_cache_ops.h
@@ -131,11 +132,37 @@ def desc(t: torch.Tensor) -> DaricTensor:
     return d
 
 
-def i64_array(values) -> ctypes.Array:
-    vals = [int(v) for v in values]
-    return (c_int64 * max(len(vals), 1))(*vals)
+class I64:
+    """Contiguous int64 copy of a sequence of ints for an `const int64_t*`
+    argument; `ptr` stays valid while the object is alive. Non-integer values
+    raise TypeError (the reference's pybind11 list<int64> conversion refuses
+    them too)."""
+    __slots__ = ("buf", "ptr", "n")
+
+    def __init__(self, values):
+        buf = array.array("q", values)
+        self.n = len(buf)
+        if self.n == 0:
+            buf = array.array("q", [0])
+        self.buf = buf
+        self.ptr = buf.buffer_info()[0]
+
+
+_NAME_CACHE: dict = {}
+_NAME_CACHE_MAX = 256
 
 
 def str_array(names) -> ctypes.Array:
-    enc = [str(n).encode() for n in names]
-    return (c_char_p * max(len(enc), 1))(*enc)
+    """NUL-terminated C strings of `names` as a `const char* const*` array.
+    Arrays are cached per distinct name tuple: callers pass the same layer
+    name lists on every call, and encoding them dominated the call cost."""
+    key = tuple(names)
+    hit = _NAME_CACHE.get(key)
+    if hit is not None:
+        return hit
+    enc = [str(n).encode() for n in key]
+    arr = (c_char_p * max(len(enc), 1))(*enc)
+    if len(_NAME_CACHE) >= _NAME_CACHE_MAX:
+        _NAME_CACHE.clear()
+    _NAME_CACHE[key] = arr
+    return arr

@@ -24,8 +24,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import (DaricChunk, DaricRope, DaricRopeSegment, check, desc, i64_array, load,
-                   str_array)
+from ._lib import I64, DaricChunk, DaricRope, DaricRopeSegment, check, desc, load, str_array
 
 __all__ = [
     "CacheCopier", "batched_memcpy_d2h", "batched_memcpy_h2d", "rerotate_pages",
@@ -41,12 +40,25 @@ def _resolve_stream(stream: int, device: Optional[torch.device]) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_EXT_STREAMS: dict = {}
+
+
+def _ext_stream(stream: int, device: torch.device):
+    key = (int(stream), device.index)
+    s = _EXT_STREAMS.get(key)
+    if s is None:
+        if len(_EXT_STREAMS) > 64:
+            _EXT_STREAMS.clear()
+        s = _EXT_STREAMS[key] = torch.cuda.ExternalStream(stream, device=device)
+    return s
+
+
 def _record(stream: int, device: torch.device, *tensors) -> None:
     """Keep caching-allocator memory of temporaries alive until `stream` has
     consumed them (the reference's record_tensor_on_external_stream)."""
     if device is None or device.type != "cuda":
         return
-    ext = torch.cuda.ExternalStream(stream, device=device)
+    ext = _ext_stream(stream, device)
     for t in tensors:
         if t is not None and t.is_cuda:
             t.record_stream(ext)
@@ -121,9 +133,9 @@ class CacheCopier:
         dev = self._device(names)
         st = _resolve_stream(stream, dev)
         idx = desc(indices_flat)
-        status = fn(self._h, str_array(names), len(names), i64_array(offsets), len(offsets),
-                    i64_array(byte_sizes), len(byte_sizes), ctypes.byref(idx),
-                    i64_array(indices_offsets), len(indices_offsets), *extra, ctypes.c_uint64(st))
+        off, sz, ioff = I64(offsets), I64(byte_sizes), I64(indices_offsets)
+        status = fn(self._h, str_array(names), len(names), off.ptr, off.n, sz.ptr, sz.n,
+                    ctypes.byref(idx), ioff.ptr, ioff.n, *extra, ctypes.c_uint64(st))
         check(status)
         if names:
             _record(st, dev, indices_flat)
@@ -154,9 +166,9 @@ class CacheCopier:
                 raise RuntimeError("deltas and num_tokens must have one entry per job")
         dev = self._device(names)
         rope = _rope(inv_freq, rotary_dim, is_neox_style, dev) if names else DaricRope()
+        dl, nt = I64(deltas), I64(num_tokens)
         self._copy(self._lib.daric_copier_scatter_pages_rerotate, names, offsets, byte_sizes,
-                   indices_flat, indices_offsets, stream,
-                   extra=(i64_array(deltas), i64_array(num_tokens), ctypes.byref(rope)))
+                   indices_flat, indices_offsets, stream, extra=(dl.ptr, nt.ptr, ctypes.byref(rope)))
         if names and dev is not None:
             _record(_resolve_stream(stream, dev), dev, inv_freq)
 
@@ -170,12 +182,11 @@ def _memcpy(fn, dev_t, host_t, dev_offsets, host_offsets, sizes, stream, d2h):
     dev = dev_t.device if dev_t.is_cuda else None
     st = _resolve_stream(stream, dev)
     a, b = desc(dev_t), desc(host_t)
+    do, ho, sz = I64(dev_offsets), I64(host_offsets), I64(sizes)
     if d2h:
-        check(fn(ctypes.byref(a), ctypes.byref(b), i64_array(dev_offsets), i64_array(host_offsets),
-                 i64_array(sizes), n, ctypes.c_uint64(st)))
+        check(fn(ctypes.byref(a), ctypes.byref(b), do.ptr, ho.ptr, sz.ptr, n, ctypes.c_uint64(st)))
     else:
-        check(fn(ctypes.byref(b), ctypes.byref(a), i64_array(host_offsets), i64_array(dev_offsets),
-                 i64_array(sizes), n, ctypes.c_uint64(st)))
+        check(fn(ctypes.byref(b), ctypes.byref(a), ho.ptr, do.ptr, sz.ptr, n, ctypes.c_uint64(st)))
 
 
 def batched_memcpy_d2h(staging: torch.Tensor, shm: torch.Tensor, stg_offsets: Sequence[int],

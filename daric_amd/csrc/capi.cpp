@@ -7,6 +7,7 @@
 #include <limits>
 #include <map>
 #include <string>
+#include <string_view>
 #include <tuple>
 #include <unordered_map>
 
@@ -214,8 +215,26 @@ struct daric_copier {
         bool page_first;
         const float* k_scale = nullptr;
         int64_t k_scale_numel = 0;
+        // Page-copy shape of the tensor, computed once at registration. A
+        // layout the copy path rejects keeps its error here; it is raised when
+        // a job uses the layer, as the reference raises it at call time.
+        PageShape shape{};
+        int shape_status = DARIC_OK;
+        std::string shape_msg;
+        // Rotary row geometry for the last (rotary_dim, is_neox) the fused
+        // path asked for (geom_rot == 0: not computed yet).
+        int geom_rot = 0;
+        int geom_neox = -1;
+        int geom_status = DARIC_OK;
+        std::string geom_msg;   // rope_layout error, or why row_geometry refused
+        bool geom_ok = false;
+        RopeLayout lay{};
+        RowGeom geom{};
     };
     std::unordered_map<std::string, Layer> layers;
+    // Lookup index keyed by views of the map's own key strings (the map's
+    // nodes are stable), so resolving a const char* allocates nothing.
+    std::unordered_map<std::string_view, Layer*> by_name;
     daric_tensor store{};
     bool has_store = false;
     std::mutex mu;  // registration vs. lookups from concurrent calls
@@ -225,9 +244,10 @@ namespace {
 
 struct ResolvedJobs {
     std::vector<CopyJob> jobs;
-    std::vector<const daric_copier::Layer*> layers;
+    std::vector<daric_copier::Layer*> layers;
     int64_t max_tiles = 0;
     int64_t max_elements = 0;
+    int64_t max_span = 0;
     int vw = 16;
     int device = -1;
 };
@@ -255,9 +275,9 @@ ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_j
     r.layers.reserve(n_jobs);
     for (int64_t i = 0; i < n_jobs; ++i) {
         DARIC_CHECK(names[i] != nullptr, "layer not registered: (null)");
-        auto it = c->layers.find(names[i]);
-        DARIC_CHECK(it != c->layers.end(), "layer not registered: ", names[i]);
-        r.layers.push_back(&it->second);
+        auto it = c->by_name.find(std::string_view(names[i]));
+        DARIC_CHECK(it != c->by_name.end(), "layer not registered: ", names[i]);
+        r.layers.push_back(it->second);
     }
     r.device = r.layers[0]->t.device;
     DARIC_CHECK(indices->device == r.device, "indices_flat must be on the same device as kvcache");
@@ -274,7 +294,9 @@ ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_j
     bool a16 = aligned(store, 16), a4 = aligned(store, 4);
     for (int64_t i = 0; i < n_jobs; ++i) {
         const daric_tensor& t = r.layers[i]->t;
-        const PageShape s = page_copy_shape(t, r.layers[i]->page_first);
+        if (r.layers[i]->shape_status != DARIC_OK)
+            throw Error(r.layers[i]->shape_status, r.layers[i]->shape_msg);
+        const PageShape& s = r.layers[i]->shape;
         const int64_t n_sel = indices_offsets[i + 1] - indices_offsets[i];
         const int64_t num = s.prefix_size * n_sel * s.suffix;
         if (byte_sizes[i] != num)
@@ -299,6 +321,7 @@ ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_j
         j.delta = 0.0f;
         r.max_tiles = std::max(r.max_tiles, s.prefix_size * n_sel);
         r.max_elements = std::max(r.max_elements, num);
+        r.max_span = std::max(r.max_span, s.suffix);
         const auto al = [&](int64_t a) {
             return s.suffix % a == 0 && s.page_stride % a == 0 && s.prefix_stride % a == 0 &&
                    offsets[i] % a == 0 && aligned(t.data, a);
@@ -324,9 +347,8 @@ int copy_pages(daric_copier* c, const char* const* names, int64_t n_jobs, const 
         DeviceGuard guard(r.device);
         const hipStream_t st = as_stream(stream);
         DescUpload up(r.device, r.jobs.data(), r.jobs.size() * sizeof(CopyJob), st);
-        LaunchTimer timer(st);
         launch_copy_pages(static_cast<const CopyJob*>(up.get()), static_cast<int>(r.jobs.size()),
-                          static_cast<int>(r.max_tiles), r.vw, gather, st);
+                          static_cast<int>(r.max_tiles), r.max_span, r.vw, gather, st);
     });
 }
 
@@ -397,13 +419,22 @@ int daric_copier_register_layer(daric_copier* c, const char* name, const daric_t
         check_tensor_struct(tensor, "kvcache tensor");
         DARIC_CHECK(tensor->device >= 0, "kvcache tensor must be on GPU: ", name);
         std::lock_guard<std::mutex> lk(c->mu);
-        daric_copier::Layer L{*tensor, is_page_first != 0, nullptr, 0};
+        daric_copier::Layer L;
+        L.t = *tensor;
+        L.page_first = is_page_first != 0;
+        try {
+            L.shape = page_copy_shape(L.t, L.page_first);
+        } catch (const Error& e) {
+            L.shape_status = e.status;
+            L.shape_msg = e.what();
+        }
         auto it = c->layers.find(name);
         if (it != c->layers.end()) {
             L.k_scale = it->second.k_scale;
             L.k_scale_numel = it->second.k_scale_numel;
         }
-        c->layers.insert_or_assign(name, L);
+        auto res = c->layers.insert_or_assign(name, std::move(L));
+        c->by_name[std::string_view(res.first->first)] = &res.first->second;
     });
 }
 
@@ -474,56 +505,72 @@ int daric_copier_scatter_pages_rerotate(daric_copier* c, const char* const* name
         check_rope(rope);
         DARIC_CHECK(deltas != nullptr && num_tokens != nullptr, "deltas and num_tokens must not be null");
         DARIC_CHECK(r.vw == 16, "fused scatter+rerotate needs 16-byte aligned pages, strides and offsets");
-        // Group jobs by row geometry and element type; one launch per group.
-        using Key = std::tuple<int, int, int, int, int, int, int, int, int>;
-        std::map<Key, std::vector<int64_t>> groups;
-        std::map<Key, RowGeom> geoms;
+        // Group jobs by row geometry and element type; one launch per group
+        // (normally one: every layer of a model shares its geometry).
+        struct Group {
+            int kind;
+            RowGeom g;
+            std::vector<CopyJob> jobs;
+            int64_t max_tiles = 0;
+        };
+        std::vector<Group> groups;
         for (int64_t i = 0; i < n_jobs; ++i) {
-            const auto* L = r.layers[i];
+            daric_copier::Layer* L = r.layers[i];
             const int kind = elem_kind(L->t);
             DARIC_CHECK(kind >= 0, "unsupported KV cache dtype for rerotate at job ", i);
             DARIC_CHECK(deltas[i] > -(1ll << 24) && deltas[i] < (1ll << 24),
                         "delta out of range at job ", i, ": ", deltas[i]);
             DARIC_CHECK(num_tokens[i] >= 0, "negative num_tokens at job ", i);
-            const RopeLayout lay = rope_layout(L->t, L->page_first, rope->rotary_dim);
-            DARIC_CHECK(L->k_scale == nullptr || L->k_scale_numel >= lay.H,
+            const int neox = rope->is_neox != 0 ? 1 : 0;
+            if (L->geom_rot != rope->rotary_dim || L->geom_neox != neox) {
+                L->geom_rot = rope->rotary_dim;
+                L->geom_neox = neox;
+                L->geom_status = DARIC_OK;
+                L->geom_msg.clear();
+                L->geom_ok = false;
+                try {
+                    L->lay = rope_layout(L->t, L->page_first, rope->rotary_dim);
+                    L->geom_ok = row_geometry(L->t, L->page_first, L->lay, rope->rotary_dim, neox != 0,
+                                              L->shape.suffix, &L->geom, &L->geom_msg);
+                } catch (const Error& e) {
+                    L->geom_status = e.status;
+                    L->geom_msg = e.what();
+                }
+            }
+            if (L->geom_status != DARIC_OK) throw Error(L->geom_status, L->geom_msg);
+            DARIC_CHECK(L->k_scale == nullptr || L->k_scale_numel >= L->lay.H,
                         "k_scale of job ", i, " has ", L->k_scale_numel, " entries, the layer has ",
-                        lay.H, " heads");
-            RowGeom g{};
-            std::string why;
-            DARIC_CHECK(row_geometry(L->t, L->page_first, lay, rope->rotary_dim, rope->is_neox != 0,
-                                     r.jobs[i].span, &g, &why),
-                        "fused scatter+rerotate does not support the layout of job ", i, " (",
-                        why, "); use scatter_pages followed by rerotate_pages");
+                        L->lay.H, " heads");
+            DARIC_CHECK(L->geom_ok, "fused scatter+rerotate does not support the layout of job ", i, " (",
+                        L->geom_msg, "); use scatter_pages followed by rerotate_pages");
             CopyJob& j = r.jobs[i];
             j.delta = static_cast<float>(deltas[i]);
             j.n_tokens = static_cast<int32_t>(std::min<int64_t>(num_tokens[i], kIntMax));
-            const Key key{kind, g.W, g.n_rows, g.krows, g.tok_div, g.PS, g.H, g.R, g.ipr};
-            groups[key].push_back(i);
-            geoms[key] = g;
+            Group* grp = nullptr;
+            for (auto& gr : groups)
+                if (gr.kind == kind && std::memcmp(&gr.g, &L->geom, sizeof(RowGeom)) == 0) { grp = &gr; break; }
+            if (grp == nullptr) {
+                groups.push_back(Group{kind, L->geom, {}, 0});
+                grp = &groups.back();
+                grp->jobs.reserve(n_jobs);
+            }
+            grp->jobs.push_back(j);
+            grp->max_tiles = std::max<int64_t>(grp->max_tiles, int64_t(j.prefix) * j.n_sel);
         }
         DeviceGuard guard(r.device);
         const hipStream_t st = as_stream(stream);
-        for (const auto& [key, members] : groups) {
-            std::vector<CopyJob> gj;
-            gj.reserve(members.size());
-            int64_t max_tiles = 0;
-            for (int64_t i : members) {
-                gj.push_back(r.jobs[i]);
-                max_tiles = std::max<int64_t>(max_tiles, int64_t(r.jobs[i].prefix) * r.jobs[i].n_sel);
-            }
-            if (max_tiles == 0) continue;
+        for (const Group& gr : groups) {
+            if (gr.max_tiles == 0) continue;
             RowGeomDiv gd;
-            gd.g = geoms[key];
+            gd.g = gr.g;
             gd.ipr = FastDiv(gd.g.ipr);
             gd.tok_div = FastDiv(gd.g.tok_div);
             gd.ps = FastDiv(gd.g.PS);
             gd.h = FastDiv(gd.g.H);
-            DescUpload up(r.device, gj.data(), gj.size() * sizeof(CopyJob), st);
-            LaunchTimer timer(st);
-            launch_scatter_rotate(static_cast<const CopyJob*>(up.get()), static_cast<int>(gj.size()),
-                                  static_cast<int>(max_tiles), gd, std::get<0>(key),
-                                  rope->is_neox != 0, rope->inv_freq, st);
+            DescUpload up(r.device, gr.jobs.data(), gr.jobs.size() * sizeof(CopyJob), st);
+            launch_scatter_rotate(static_cast<const CopyJob*>(up.get()), static_cast<int>(gr.jobs.size()),
+                                  static_cast<int>(gr.max_tiles), gd, gr.kind, rope->is_neox != 0,
+                                  rope->inv_freq, st);
         }
     });
 }
@@ -687,7 +734,6 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
         DescUpload up(t.device, blob.data(), blob.size(), st);
         const auto* d_segs = static_cast<const RopeSeg*>(up.get());
         auto* const* d_layers = reinterpret_cast<uint8_t* const*>(static_cast<uint8_t*>(up.get()) + seg_bytes);
-        LaunchTimer timer(st);
         launch_rerotate_inplace(d_layers, static_cast<int>(n_layers), g, d_segs,
                                 static_cast<int>(segs.size()), static_cast<int>(tiles),
                                 static_cast<const int32_t*>(block_table->data), rope->inv_freq,
@@ -802,7 +848,6 @@ int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_fi
         std::memcpy(blob.data() + cb, ptrs.data(), n_layers * sizeof(uint8_t*));
         DescUpload up(t.device, blob.data(), blob.size(), st);
         auto* const* d_layers = reinterpret_cast<uint8_t* const*>(static_cast<uint8_t*>(up.get()) + cb);
-        LaunchTimer timer(st);
         launch_deviation(d_layers, static_cast<int>(n_layers), g, ck,
                          static_cast<const int32_t*>(block_table->data),
                          static_cast<const uint8_t*>(k_new->data), nk, T,
@@ -831,7 +876,6 @@ int daric_topk_per_chunk(const daric_tensor* keys, const daric_chunk* chunks, in
         DeviceGuard guard(keys->device);
         const hipStream_t st = as_stream(stream);
         DescUpload up(keys->device, c.v.data(), c.v.size() * sizeof(SelChunk), st);
-        LaunchTimer timer(st);
         launch_topk(static_cast<const float*>(keys->data), static_cast<int>(L), T,
                     static_cast<const SelChunk*>(up.get()), static_cast<int>(n_chunks),
                     static_cast<int>(std::max<int64_t>(c.max_tokens, 1)),
@@ -876,7 +920,6 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
         std::memcpy(blob.data() + cb, ptrs.data(), n_layers * sizeof(uint8_t*));
         DescUpload up(t.device, blob.data(), blob.size(), st);
         auto* const* d_layers = reinterpret_cast<uint8_t* const*>(static_cast<uint8_t*>(up.get()) + cb);
-        LaunchTimer timer(st);
         launch_merge(d_layers, static_cast<int>(n_layers), g, t.elem_size,
                      static_cast<const int32_t*>(block_table->data),
                      static_cast<const uint8_t*>(k_new->data),

@@ -124,14 +124,6 @@ private:
     void* ptr_ = nullptr;
 };
 
-// Kernel timing (daric_timing_enable / daric_timing_read).
-struct LaunchTimer {
-    hipEvent_t start = nullptr;
-    hipStream_t stream = nullptr;
-    explicit LaunchTimer(hipStream_t s);
-    ~LaunchTimer();
-};
-
 // Sets the current device for the scope and restores the previous one.
 class DeviceGuard {
 public:

@@ -1,19 +1,30 @@
 // Paged-KV gather / scatter and the fused scatter + K re-rotation (gfx950).
 //
-// Work decomposition: blockIdx.y is the job (one (layer, chunk) pair),
-// blockIdx.x a tile = one page span of one prefix index (K or V half of a
-// page for vLLM's [2, blocks, PS, H, D] layout: 32 KiB at Llama-3-8B shape).
-// A 256-lane workgroup streams the span with 16-byte accesses, 8 in flight
-// per lane (32 KiB per round), loads before stores. Cache-side stores and
-// staging-side loads are marked nontemporal: every byte is touched once.
+// Work decomposition: a job is one (layer, chunk) pair; a tile is one page
+// span of one prefix index (the K or V half of a page for vLLM's
+// [2, blocks, PS, H, D] layout: 32 KiB at Llama-3-8B shape). A 256-lane
+// workgroup streams a tile, or a part of one, with 16-byte accesses, 8 in
+// flight per lane, loads before stores. Staging-side loads and cache-side
+// stores are nontemporal: every byte is touched once.
+//
+// Block order (measured on MI355X at the Llama-3-8B shape, 256 jobs of
+// 64 pages): the scatter direction runs job-minor -- consecutive workgroups
+// take the same tile of consecutive jobs -- which sustained ~6.3 TB/s against
+// ~6.0 TB/s for a tile-major order; the gather direction runs tile-major within
+// a job and cuts each tile into parts of ~8 KiB, which sustained ~6.3 TB/s
+// against ~5.7 TB/s for whole-tile workgroups.
+//
 // Pages whose block id is 0 (vLLM's null block) are skipped, as the
 // reference's kernels skip them (csrc/cache_ops/kernels.cu:26,39,69,79,104,117);
 // ids outside [0, num_pages) are skipped as well instead of faulting.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "elem.h"
 #include "jobs.h"
 #include "kernels.h"
+#include "launch.h"
 
 namespace daric {
 
@@ -32,31 +43,36 @@ __device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_lo
 template <typename T>
 __device__ __forceinline__ void st_nt(T* p, T v) { __builtin_nontemporal_store(v, p); }
 
-// Copies `span` bytes (a multiple of VW, < 2^31) from src to dst.
+// Copies n_units units of VW bytes from src to dst (n_units < 2^31).
 template <int VW>
-__device__ __forceinline__ void copy_span(const uint8_t* __restrict__ src,
-                                          uint8_t* __restrict__ dst, int64_t span) {
+__device__ __forceinline__ void copy_units(const uint8_t* __restrict__ src,
+                                           uint8_t* __restrict__ dst, int n_units) {
     using T = typename VecOf<VW>::T;
     const T* s = reinterpret_cast<const T*>(src);
     T* d = reinterpret_cast<T*>(dst);
-    const int n = static_cast<int>(span / VW);
-    for (int base = 0; base < n; base += kThreads * kUnroll) {
+    for (int base = 0; base < n_units; base += kThreads * kUnroll) {
         T v[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int i = base + u * kThreads + static_cast<int>(threadIdx.x);
-            if (i < n) v[u] = ld_nt(s + i);
+            if (i < n_units) v[u] = ld_nt(s + i);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int i = base + u * kThreads + static_cast<int>(threadIdx.x);
-            if (i < n) st_nt(d + i, v[u]);
+            if (i < n_units) st_nt(d + i, v[u]);
         }
     }
 }
 
-// Resolves tile blockIdx.x of job blockIdx.y. Returns false when the tile is
-// beyond the job or its page is skipped.
+template <int VW>
+__device__ __forceinline__ void copy_span(const uint8_t* __restrict__ src,
+                                          uint8_t* __restrict__ dst, int64_t span) {
+    copy_units<VW>(src, dst, static_cast<int>(span / VW));
+}
+
+// Resolves tile t of job j. Returns false when the tile is beyond the job or
+// its page is skipped.
 __device__ __forceinline__ bool resolve_tile(const CopyJob& j, int t, int& p, int& s,
                                              uint8_t*& cache, uint8_t*& stage) {
     const int n_sel = j.n_sel;
@@ -70,35 +86,67 @@ __device__ __forceinline__ bool resolve_tile(const CopyJob& j, int t, int& p, in
     return true;
 }
 
-template <int VW, bool GATHER>
-__global__ __launch_bounds__(kThreads) void copy_pages_kernel(const CopyJob* __restrict__ jobs) {
-    const CopyJob& j = jobs[blockIdx.y];
-    int p, s;
-    uint8_t *cache, *stage;
-    if (!resolve_tile(j, static_cast<int>(blockIdx.x), p, s, cache, stage)) return;
-    if (GATHER)
-        copy_span<VW>(cache, stage, j.span);
-    else
-        copy_span<VW>(stage, cache, j.span);
+// Block -> (job, unit) mapping. Job-minor: block b takes job b % n_jobs and
+// unit b / n_jobs; tile-major: job blockIdx.y, unit blockIdx.x. A unit is part
+// (unit & (parts - 1)) of tile (unit >> log2 parts).
+template <bool JOB_MINOR>
+__device__ __forceinline__ void block_unit(const FastDiv& njobs, int& job, int& unit) {
+    if (JOB_MINOR) {
+        const uint32_t b = blockIdx.x;
+        const uint32_t q = njobs.div(b);
+        job = static_cast<int>(b - q * njobs.d);
+        unit = static_cast<int>(q);
+    } else {
+        job = static_cast<int>(blockIdx.y);
+        unit = static_cast<int>(blockIdx.x);
+    }
 }
 
-// Fused scatter + rotation. A work item of a K row is either a rotated item
-// (NeoX: the two 16-byte units holding pairs (i, i + R/2) for i in
-// [k*VE, k*VE + VE); GPT-J: one unit holding VE/2 adjacent pairs) or a
-// pass-through unit of the row's unrotated tail. Rows that are not rotated
-// (V rows, tokens past the job's n_tokens) are copied bit-exactly.
+template <int VW, bool GATHER, bool JOB_MINOR>
+__global__ __launch_bounds__(kThreads) void copy_pages_kernel(const CopyJob* __restrict__ jobs,
+                                                              FastDiv njobs, int log2_parts) {
+    int jb, unit;
+    block_unit<JOB_MINOR>(njobs, jb, unit);
+    const CopyJob& j = jobs[jb];
+    int p, s;
+    uint8_t *cache, *stage;
+    if (!resolve_tile(j, unit >> log2_parts, p, s, cache, stage)) return;
+    const int n_units = static_cast<int>(j.span / VW);
+    const int parts = 1 << log2_parts;
+    const int per = (n_units + parts - 1) >> log2_parts;
+    const int u0 = (unit & (parts - 1)) * per;
+    const int cnt = min(per, n_units - u0);
+    if (cnt <= 0) return;
+    const int64_t b0 = static_cast<int64_t>(u0) * VW;
+    if (GATHER)
+        copy_units<VW>(cache + b0, stage + b0, cnt);
+    else
+        copy_units<VW>(stage + b0, cache + b0, cnt);
+}
+
+// Fused scatter + rotation, job-minor block order. A work item of a K row is
+// either a rotated item (NeoX: the two 16-byte units holding pairs
+// (i, i + R/2) for i in [k*VE, k*VE + VE); GPT-J: one unit holding VE/2
+// adjacent pairs) or a pass-through unit of the row's unrotated tail. Rows
+// that are not rotated (V rows, tokens past the job's n_tokens) are copied
+// bit-exactly. The first round's loads are issued before the workgroup
+// computes the tile's cos/sin values into LDS, so the sincos latency overlaps
+// the memory latency.
 template <int KIND, bool NEOX>
 __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
-    const CopyJob* __restrict__ jobs, RowGeomDiv gd, const float* __restrict__ inv_freq) {
+    const CopyJob* __restrict__ jobs, FastDiv njobs, RowGeomDiv gd,
+    const float* __restrict__ inv_freq) {
     using E = Elem<KIND>;
     constexpr int VE = E::VE;
     __shared__ float s_cos[kMaxHalfRot];
     __shared__ float s_sin[kMaxHalfRot];
 
-    const CopyJob& j = jobs[blockIdx.y];
+    int jb, unit;
+    block_unit<true>(njobs, jb, unit);
+    const CopyJob& j = jobs[jb];
     int p, s;
     uint8_t *cache, *stage;
-    if (!resolve_tile(j, static_cast<int>(blockIdx.x), p, s, cache, stage)) return;
+    if (!resolve_tile(j, unit, p, s, cache, stage)) return;
 
     const RowGeom& g = gd.g;
     const int n_valid = min(max(j.n_tokens - s * g.PS, 0), g.PS);
@@ -108,14 +156,6 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
     }
 
     const int half = g.R / 2;
-    for (int i = threadIdx.x; i < half; i += kThreads) {
-        float sn, cs;
-        sincosf(j.delta * inv_freq[i], &sn, &cs);
-        s_cos[i] = cs;
-        s_sin[i] = sn;
-    }
-    __syncthreads();
-
     const u32x4* __restrict__ src = reinterpret_cast<const u32x4*>(stage);
     u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(cache);
     const int upr = g.W / VE;                      // 16-byte units per row
@@ -152,6 +192,15 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
                 a[u] = ld_nt(src + ua[u]);
                 if (pair[u]) b[u] = ld_nt(src + ua[u] + partner);
             }
+        }
+        if (base == 0) {
+            for (int i = threadIdx.x; i < half; i += kThreads) {
+                float sn, cs;
+                sincosf(j.delta * inv_freq[i], &sn, &cs);
+                s_cos[i] = cs;
+                s_sin[i] = sn;
+            }
+            __syncthreads();
         }
 #pragma unroll
         for (int u = 0; u < kRotUnroll; ++u) {
@@ -200,40 +249,208 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
     }
 }
 
-void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int vw, bool gather,
-                       hipStream_t stream) {
-    constexpr int kMaxY = 65535;
-    for (int j0 = 0; j0 < n_jobs; j0 += kMaxY) {
-        const int nj = n_jobs - j0 < kMaxY ? n_jobs - j0 : kMaxY;
-        const dim3 grid(static_cast<unsigned>(max_tiles), static_cast<unsigned>(nj));
-        const CopyJob* jp = d_jobs + j0;
-        if (vw == 16) {
-            if (gather) copy_pages_kernel<16, true><<<grid, kThreads, 0, stream>>>(jp);
-            else copy_pages_kernel<16, false><<<grid, kThreads, 0, stream>>>(jp);
-        } else if (vw == 4) {
-            if (gather) copy_pages_kernel<4, true><<<grid, kThreads, 0, stream>>>(jp);
-            else copy_pages_kernel<4, false><<<grid, kThreads, 0, stream>>>(jp);
-        } else {
-            if (gather) copy_pages_kernel<1, true><<<grid, kThreads, 0, stream>>>(jp);
-            else copy_pages_kernel<1, false><<<grid, kThreads, 0, stream>>>(jp);
-        }
-        check_launch(gather ? "gather_pages" : "scatter_pages");
+// Lane-exchange variant of the fused kernel, used when the 16-byte units of a
+// row (upr = W / VE) divide the 64-lane wavefront. Lanes keep the plain
+// copy's access pattern -- unit i of the tile is lane i % 256 of round
+// i / 256, fully coalesced -- so a lane's position k = i % upr inside its row
+// is fixed, and so are its rotary pair indices: its cos/sin values are read
+// from LDS into registers once per tile. NeoX pair halves (units k and
+// k +- n_rot of the same row, always in the same wavefront) are exchanged with
+// ds_bpermute. GPT-J pairs are adjacent elements of one unit and need no
+// exchange. Rows that are not rotated are stored as loaded.
+#ifndef DARIC_ROT_LANE_UNROLL
+#define DARIC_ROT_LANE_UNROLL 4
+#endif
+template <int KIND, bool NEOX>
+__global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
+    const CopyJob* __restrict__ jobs, FastDiv njobs, RowGeomDiv gd,
+    const float* __restrict__ inv_freq) {
+    using E = Elem<KIND>;
+    constexpr int VE = E::VE;
+    constexpr int NC = NEOX ? VE : VE / 2;  // cos/sin values per lane
+    constexpr int UNR = DARIC_ROT_LANE_UNROLL;
+    __shared__ float s_cos[kMaxHalfRot];
+    __shared__ float s_sin[kMaxHalfRot];
+
+    int jb, unit;
+    block_unit<true>(njobs, jb, unit);
+    const CopyJob& j = jobs[jb];
+    int p, s;
+    uint8_t *cache, *stage;
+    if (!resolve_tile(j, unit, p, s, cache, stage)) return;
+
+    const RowGeom& g = gd.g;
+    const int n_valid = min(max(j.n_tokens - s * g.PS, 0), g.PS);
+    if (p != 0 || n_valid == 0 || j.delta == 0.0f || g.krows == 0) {
+        copy_span<16>(stage, cache, j.span);
+        return;
     }
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63;
+    const int upr = g.W / VE;                       // a power of two <= 64
+    const int log2_upr = __builtin_ctz(static_cast<unsigned>(upr));
+    const int k = tid & (upr - 1);
+    const int nr = g.n_rot;
+    const bool rot_lane = NEOX ? k < 2 * nr : k < nr;
+    const bool first = k < nr;
+    const int src_lane = (NEOX && rot_lane) ? (first ? lane + nr : lane - nr) : lane;
+    const int pi0 = NEOX ? (first ? k : k - nr) * VE : k * (VE / 2);
+    const int n_units = static_cast<int>(j.span / 16);
+    const int half = g.R / 2;
+    const float* __restrict__ ksc = j.k_scale;
+    const u32x4* __restrict__ src = reinterpret_cast<const u32x4*>(stage);
+    u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(cache);
+
+    float cs[NC], ss[NC];
+    for (int base = 0; base < n_units; base += kThreads * UNR) {
+        u32x4 v[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int i = base + u * kThreads + tid;
+            v[u] = u32x4{0u, 0u, 0u, 0u};
+            if (i < n_units) v[u] = ld_nt(src + i);
+        }
+        if (base == 0) {
+            for (int i = tid; i < half; i += kThreads) {
+                float sn, c;
+                sincosf(j.delta * inv_freq[i], &sn, &c);
+                s_cos[i] = c;
+                s_sin[i] = sn;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < NC; ++e) {
+                const int pi = rot_lane ? pi0 + e : 0;
+                cs[e] = s_cos[pi];
+                ss[e] = (NEOX && first) ? -s_sin[pi] : s_sin[pi];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int i = base + u * kThreads + tid;
+            u32x4 pv = v[u];
+            if (NEOX) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    pv[w] = static_cast<uint32_t>(__shfl(static_cast<int>(v[u][w]), src_lane, 64));
+            }
+            if (i >= n_units) continue;
+            const uint32_t r = static_cast<uint32_t>(i >> log2_upr);
+            const uint32_t q = gd.tok_div.div(r);
+            const int token = static_cast<int>(q - gd.ps.div(q) * g.PS);
+            const bool rot = rot_lane && static_cast<int>(r) < g.krows && token < n_valid;
+            if (!rot) {
+                st_nt(dst + i, v[u]);
+                continue;
+            }
+            float scale = 1.0f;
+            if (KIND == kE4M3 && ksc != nullptr) {
+                const int h = g.tok_div == 1
+                    ? static_cast<int>(gd.ps.div(r) - gd.h.div(gd.ps.div(r)) * g.H)
+                    : static_cast<int>(r - gd.h.div(r) * g.H);
+                scale = ksc[h];
+            }
+            float x[VE];
+            E::unpack(v[u], x, scale);
+            if (NEOX) {
+                float y[VE];
+                E::unpack(pv, y, scale);
+#pragma unroll
+                for (int e = 0; e < VE; ++e) x[e] = x[e] * cs[e] + y[e] * ss[e];
+            } else {
+#pragma unroll
+                for (int m = 0; m < VE / 2; ++m) {
+                    const float x1 = x[2 * m], x2 = x[2 * m + 1];
+                    x[2 * m] = x1 * cs[m] - x2 * ss[m];
+                    x[2 * m + 1] = x2 * cs[m] + x1 * ss[m];
+                }
+            }
+            st_nt(dst + i, E::pack(x, 1.0f / scale));
+        }
+    }
+}
+
+// Descriptor upload: one 16-byte unit per lane, read from host memory.
+__global__ __launch_bounds__(kThreads) void upload_kernel(const u32x4* __restrict__ src,
+                                                         u32x4* __restrict__ dst, uint32_t n16) {
+    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < n16) dst[i] = src[i];
+}
+
+// Largest grid.x: grid.x * 256 lanes must stay below 2^32.
+constexpr int64_t kMaxBlocksX = (1ll << 24) - 1;
+constexpr int kMaxY = 65535;
+
+void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int64_t max_span, int vw,
+                       bool gather, hipStream_t stream) {
+    if (!gather) {
+        // job-minor: slices of jobs so that max_tiles * slice fits grid.x
+        const int slice = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(n_jobs, kMaxBlocksX / max_tiles)));
+        for (int j0 = 0; j0 < n_jobs; j0 += slice) {
+            const int nj = std::min(slice, n_jobs - j0);
+            const FastDiv fd(static_cast<uint32_t>(nj));
+            const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(max_tiles) * nj));
+            const CopyJob* jp = d_jobs + j0;
+            if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, false, true>), grid, kThreads, 0, stream, jp, fd, 0);
+            else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, false, true>), grid, kThreads, 0, stream, jp, fd, 0);
+            else DARIC_LAUNCH((copy_pages_kernel<1, false, true>), grid, kThreads, 0, stream, jp, fd, 0);
+            check_launch("scatter_pages");
+        }
+        return;
+    }
+    // tile-major within a job, tiles cut into parts of about 8 KiB
+    int log2_parts = 0;
+    while (log2_parts < 3 && (max_span >> (log2_parts + 1)) >= 8192 &&
+           (static_cast<int64_t>(max_tiles) << (log2_parts + 1)) <= kMaxBlocksX)
+        ++log2_parts;
+    const FastDiv fd(1);
+    for (int j0 = 0; j0 < n_jobs; j0 += kMaxY) {
+        const int nj = std::min(kMaxY, n_jobs - j0);
+        const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(max_tiles) << log2_parts),
+                        static_cast<unsigned>(nj));
+        const CopyJob* jp = d_jobs + j0;
+        if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, true, false>), grid, kThreads, 0, stream, jp, fd, log2_parts);
+        else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, true, false>), grid, kThreads, 0, stream, jp, fd, log2_parts);
+        else DARIC_LAUNCH((copy_pages_kernel<1, true, false>), grid, kThreads, 0, stream, jp, fd, log2_parts);
+        check_launch("gather_pages");
+    }
+}
+
+void launch_upload(const void* src, void* dst, size_t n16, hipStream_t stream) {
+    if (n16 == 0) return;
+    const dim3 grid(static_cast<unsigned>((n16 + kThreads - 1) / kThreads));
+    upload_kernel<<<grid, kThreads, 0, stream>>>(static_cast<const u32x4*>(src), static_cast<u32x4*>(dst),
+                                                 static_cast<uint32_t>(n16));
+    check_launch("descriptor upload");
 }
 
 void launch_scatter_rotate(const CopyJob* d_jobs, int n_jobs, int max_tiles,
                            const RowGeomDiv& geom, int kind, bool neox, const float* inv_freq,
                            hipStream_t stream) {
-    constexpr int kMaxY = 65535;
-    for (int j0 = 0; j0 < n_jobs; j0 += kMaxY) {
-        const int nj = n_jobs - j0 < kMaxY ? n_jobs - j0 : kMaxY;
-        const dim3 grid(static_cast<unsigned>(max_tiles), static_cast<unsigned>(nj));
+    // the lane-exchange kernel needs whole rows inside a wavefront
+    const int ve = kind == kE4M3 ? 16 : 8;
+    const int upr = geom.g.W / ve;
+    const bool lane = upr > 0 && 64 % upr == 0;
+    const int slice = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(n_jobs, kMaxBlocksX / max_tiles)));
+    for (int j0 = 0; j0 < n_jobs; j0 += slice) {
+        const int nj = std::min(slice, n_jobs - j0);
+        const FastDiv fd(static_cast<uint32_t>(nj));
+        const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(max_tiles) * nj));
         const CopyJob* jp = d_jobs + j0;
-#define DARIC_SR(K, N) scatter_rotate_kernel<K, N><<<grid, kThreads, 0, stream>>>(jp, geom, inv_freq)
-        if (kind == kBF16) { if (neox) DARIC_SR(kBF16, true); else DARIC_SR(kBF16, false); }
-        else if (kind == kF16) { if (neox) DARIC_SR(kF16, true); else DARIC_SR(kF16, false); }
-        else { if (neox) DARIC_SR(kE4M3, true); else DARIC_SR(kE4M3, false); }
+        if (lane) {
+#define DARIC_SR(K, N) DARIC_LAUNCH((scatter_rotate_lane_kernel<K, N>), grid, kThreads, 0, stream, jp, fd, geom, inv_freq)
+            if (kind == kBF16) { if (neox) DARIC_SR(kBF16, true); else DARIC_SR(kBF16, false); }
+            else if (kind == kF16) { if (neox) DARIC_SR(kF16, true); else DARIC_SR(kF16, false); }
+            else { if (neox) DARIC_SR(kE4M3, true); else DARIC_SR(kE4M3, false); }
 #undef DARIC_SR
+        } else {
+#define DARIC_SR(K, N) DARIC_LAUNCH((scatter_rotate_kernel<K, N>), grid, kThreads, 0, stream, jp, fd, geom, inv_freq)
+            if (kind == kBF16) { if (neox) DARIC_SR(kBF16, true); else DARIC_SR(kBF16, false); }
+            else if (kind == kF16) { if (neox) DARIC_SR(kF16, true); else DARIC_SR(kF16, false); }
+            else { if (neox) DARIC_SR(kE4M3, true); else DARIC_SR(kE4M3, false); }
+#undef DARIC_SR
+        }
         check_launch("scatter_pages_rerotate");
     }
 }

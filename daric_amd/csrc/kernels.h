@@ -34,9 +34,10 @@ struct RowGeomDiv {
     FastDiv ipr, tok_div, ps, h;
 };
 
-// Plain page copies. vw is the access width in bytes (16, 4 or 1).
-void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int vw, bool gather,
-                       hipStream_t stream);
+// Plain page copies. vw is the access width in bytes (16, 4 or 1); max_span
+// is the largest page span (bytes) of the jobs.
+void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int64_t max_span, int vw,
+                       bool gather, hipStream_t stream);
 
 // Fused scatter + K re-rotation; kind is an ElemKind. All jobs share `geom`.
 void launch_scatter_rotate(const CopyJob* d_jobs, int n_jobs, int max_tiles,
@@ -63,6 +64,10 @@ void launch_merge(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int e
                   const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,
                   int64_t T, const SelChunk* d_chunks, int n_chunks, const int32_t* sel_idx,
                   int kmax, hipStream_t stream);
+
+// Copies n16 16-byte units from host-pinned `src` to device `dst` on `stream`
+// (descriptor upload; both 16-byte aligned).
+void launch_upload(const void* src, void* dst, size_t n16, hipStream_t stream);
 
 // Launch-configuration error check after a <<<>>> launch.
 void check_launch(const char* what);

@@ -1,0 +1,28 @@
+// Kernel launch wrapper shared by the .hip files. Every launch goes through
+// hipExtLaunchKernelGGL so that, when kernel timing is enabled
+// (daric_timing_enable), the dispatch packet itself records start/stop
+// timestamps: the measured interval is the kernel's execution, the same
+// interval rocprofv3 reports, without the gap an event recorded before and
+// after the launch on the stream would add.
+#pragma once
+
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+
+namespace daric {
+
+// Create a start/stop event pair when timing is enabled (else both null).
+void timing_events(hipEvent_t* start, hipEvent_t* stop);
+// Hand a pair filled by a launch to daric_timing_read (no-op for nulls).
+void timing_record(hipEvent_t start, hipEvent_t stop);
+
+}  // namespace daric
+
+#define DARIC_LAUNCH(kern, grid, block, shmem, stream, ...)                                   \
+    do {                                                                                      \
+        hipEvent_t daric_ev0_ = nullptr, daric_ev1_ = nullptr;                               \
+        ::daric::timing_events(&daric_ev0_, &daric_ev1_);                                     \
+        hipExtLaunchKernelGGL(kern, dim3(grid), dim3(block), static_cast<std::uint32_t>(shmem), \
+                              stream, daric_ev0_, daric_ev1_, 0, __VA_ARGS__);                \
+        ::daric::timing_record(daric_ev0_, daric_ev1_);                                       \
+    } while (0)

@@ -13,6 +13,7 @@
 #include "elem.h"
 #include "jobs.h"
 #include "kernels.h"
+#include "launch.h"
 
 namespace daric {
 
@@ -195,8 +196,8 @@ void launch_rerotate_inplace(uint8_t* const* d_layers, int n_layers, const Inpla
         const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(nl));
         uint8_t* const* lp = d_layers + l0;
         const float* ks = k_scales ? k_scales + static_cast<int64_t>(l0) * g.H : nullptr;
-#define DARIC_RV(K, N) rerotate_vec_kernel<K, N><<<grid, kThreads, 0, stream>>>(lp, g, d_segs, n_segs, block_table, inv_freq, ks)
-#define DARIC_RE(K, N) rerotate_elem_kernel<K, N><<<grid, kThreads, 0, stream>>>(lp, g, d_segs, n_segs, block_table, inv_freq, ks)
+#define DARIC_RV(K, N) DARIC_LAUNCH((rerotate_vec_kernel<K, N>), grid, kThreads, 0, stream, lp, g, d_segs, n_segs, block_table, inv_freq, ks)
+#define DARIC_RE(K, N) DARIC_LAUNCH((rerotate_elem_kernel<K, N>), grid, kThreads, 0, stream, lp, g, d_segs, n_segs, block_table, inv_freq, ks)
         if (vec) {
             if (kind == kBF16) { if (neox) DARIC_RV(kBF16, true); else DARIC_RV(kBF16, false); }
             else if (kind == kF16) { if (neox) DARIC_RV(kF16, true); else DARIC_RV(kF16, false); }

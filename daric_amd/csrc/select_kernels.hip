@@ -17,6 +17,7 @@
 #include "elem.h"
 #include "jobs.h"
 #include "kernels.h"
+#include "launch.h"
 
 namespace daric {
 
@@ -292,7 +293,7 @@ void launch_deviation(uint8_t* const* d_layers, int n_layers, const KVGeom& g, i
                       int64_t T, const SelChunk* d_chunks, int n_chunks, int n_tiles,
                       const float* k_scales, float* keys, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_layers));
-#define DARIC_DV(C, N) deviation_kernel<C, N><<<grid, kThreads, 0, stream>>>(d_layers, g, block_table, k_new, T, d_chunks, n_chunks, k_scales, keys)
+#define DARIC_DV(C, N) DARIC_LAUNCH((deviation_kernel<C, N>), grid, kThreads, 0, stream, d_layers, g, block_table, k_new, T, d_chunks, n_chunks, k_scales, keys)
     if (new_kind == kBF16) {
         if (cache_kind == kBF16) DARIC_DV(kBF16, kBF16);
         else if (cache_kind == kF16) DARIC_DV(kF16, kBF16);
@@ -310,7 +311,7 @@ void launch_topk(const float* keys, int n_layers, int64_t T, const SelChunk* d_c
                  int n_chunks, int max_tokens, int32_t* out_idx, int kmax, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
     const size_t lds = static_cast<size_t>(max_tokens) * sizeof(uint32_t);
-    topk_kernel<<<grid, kThreads, lds, stream>>>(keys, T, d_chunks, n_chunks, out_idx, kmax);
+    DARIC_LAUNCH((topk_kernel), grid, kThreads, lds, stream, keys, T, d_chunks, n_chunks, out_idx, kmax);
     check_launch("topk_per_chunk");
 }
 
@@ -324,10 +325,10 @@ void launch_merge(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int e
                      (g.ss * elem_size) % 16 == 0 && (g.sh * elem_size) % 16 == 0 &&
                      (g.v_off < 0 || (g.v_off * elem_size) % 16 == 0);
     if (vec)
-        merge_kernel<16><<<grid, kThreads, 0, stream>>>(d_layers, g, elem_size, block_table, k_new,
+        DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d_layers, g, elem_size, block_table, k_new,
                                                         v_new, T, d_chunks, n_chunks, sel_idx, kmax);
     else
-        merge_kernel<1><<<grid, kThreads, 0, stream>>>(d_layers, g, elem_size, block_table, k_new,
+        DARIC_LAUNCH((merge_kernel<1>), grid, kThreads, 0, stream, d_layers, g, elem_size, block_table, k_new,
                                                        v_new, T, d_chunks, n_chunks, sel_idx, kmax);
     check_launch("merge_rows");
 }

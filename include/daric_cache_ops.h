@@ -84,8 +84,9 @@ typedef struct daric_rope {
 int daric_abi_version(void);
 const char* daric_last_error(void);
 
-/* Kernel timing: when enabled, every kernel launch of this library is
- * bracketed by HIP events recorded on its launch stream. daric_timing_read
+/* Kernel timing: when enabled, every kernel this library launches carries a
+ * start/stop HIP event pair in its dispatch (hipExtLaunchKernel), so the pair
+ * brackets the kernel's execution on its launch stream. daric_timing_read
  * synchronises those events and returns the summed kernel time (ms) and the
  * number of launches since the last read (or enable), then resets them.
  * This has no counterpart in the reference; it exists for measurement. */

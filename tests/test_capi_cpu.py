@@ -99,10 +99,10 @@ class CCopier:
         return self.err(self.lib.daric_copier_register_store(self.h, ctypes.byref(d)))
 
     def gather(self, names, offsets, sizes, idx, idx_off):
+        off, sz, io = _lib.I64(offsets), _lib.I64(sizes), _lib.I64(idx_off)
         return self.err(self.lib.daric_copier_gather_pages(
-            self.h, _lib.str_array(names), len(names), _lib.i64_array(offsets), len(offsets),
-            _lib.i64_array(sizes), len(sizes), ctypes.byref(idx), _lib.i64_array(idx_off),
-            len(idx_off), ctypes.c_uint64(0)))
+            self.h, _lib.str_array(names), len(names), off.ptr, off.n, sz.ptr, sz.n,
+            ctypes.byref(idx), io.ptr, io.n, ctypes.c_uint64(0)))
 
 
 def oracle_error(fn):
