@@ -157,6 +157,255 @@ def run_gpu(cfg, steps, warmup):
                 g_step_ms=gather["step_ms"], g_kern_ms=gather["kern_ms"], T=T, L=L)
 
 
+# ---------------------------------------------------------------------------
+# Other BASELINE configurations, measured beside the headline (one GPU each).
+
+CFG3 = dict(layers=32, kv_heads=8, head_dim=128, block_size=16, requests=32, chunks=6,
+            chunk_tokens=512, k_frac=0.15, noise_scale=0.1, t_df=3, dtype="bf16")
+CFG4 = dict(layers=32, kv_heads=8, head_dim=128, block_size=16, tokens=65536, num_blocks=8192,
+            dtype="bf16")
+CFG5 = dict(layers=80, kv_heads=8, head_dim=128, block_size=16, chunks=16, chunk_tokens=2048,
+            num_blocks=4 * 2048 + 1, rope_theta=500000.0, k_frac=0.10, dtype="e4m3")
+
+
+def _gbps(nbytes, ms):
+    return nbytes / (ms / 1e3) / 1e9
+
+
+def _student_t(shape, df, gen, device):
+    """Student-t samples as N / sqrt(chi2_df / df), chi2 from df squared normals."""
+    z = torch.randn(shape, generator=gen, device=device)
+    chi = torch.zeros(shape, device=device)
+    for _ in range(df):
+        chi += torch.randn(shape, generator=gen, device=device) ** 2
+    return z / torch.sqrt(chi / df)
+
+
+def run_config3(steps, warmup, seed=0):
+    """Batched selective recompute: 32 requests x 6 chunks x
+    512 tokens = 98304 tokens, Llama-3-8B KV shape, bf16. Chunk pages come from
+    a seeded permutation of the block pool and each request's chunk order is
+    shuffled by seed. Recomputed K = cached K + 0.1 * StudentT(3). One step =
+    kv_deviation + topk_per_chunk (k = 77 of 512) + merge_rows of the selected
+    K/V rows."""
+    from daric_amd import cache_ops
+    c = CFG3
+    dev = torch.device("cuda:0")
+    L, H, D, PS = c["layers"], c["kv_heads"], c["head_dim"], c["block_size"]
+    n_chunk = c["requests"] * c["chunks"]
+    T = n_chunk * c["chunk_tokens"]
+    pages_per_chunk = c["chunk_tokens"] // PS
+    NB = T // PS + 1024
+    g = torch.Generator().manual_seed(seed)
+    ids = (torch.randperm(NB - 1, generator=g)[: T // PS] + 1).to(torch.int32)
+    # per request, the stored chunks are visited in a shuffled order
+    order = []
+    for r in range(c["requests"]):
+        perm = torch.randperm(c["chunks"], generator=g).tolist()
+        order += [r * c["chunks"] + p for p in perm]
+    bt = torch.cat([ids[o * pages_per_chunk:(o + 1) * pages_per_chunk] for o in order]).to(dev)
+    k = max(1, int(round(c["k_frac"] * c["chunk_tokens"])))
+    chunks = [(i * pages_per_chunk, i * c["chunk_tokens"], c["chunk_tokens"], k) for i in range(n_chunk)]
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    layers = [torch.randn(2, NB, PS, H, D, generator=gd, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    k_new = torch.empty(L, T, H, D, dtype=torch.bfloat16, device=dev)
+    slot_blk = bt.long().repeat_interleave(PS)
+    slot_in = torch.arange(T, device=dev) % PS
+    for l in range(L):
+        base = layers[l][0][slot_blk, slot_in].float()
+        k_new[l] = (base + c["noise_scale"] * _student_t(base.shape, c["t_df"], gd, dev)).to(torch.bfloat16)
+    v_new = torch.randn(L, T, H, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    keys = torch.empty(L, T, dtype=torch.float32, device=dev)
+    sel = torch.empty(L, n_chunk, k, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    st = stream.cuda_stream
+
+    def dev_step():
+        cache_ops.kv_deviation(layers, False, bt, k_new, chunks, keys=keys, stream=st)
+
+    def topk_step():
+        cache_ops.topk_per_chunk(keys, chunks, kmax=k, out=sel, stream=st)
+
+    def merge_step():
+        cache_ops.merge_rows(layers, False, bt, k_new, v_new, chunks, sel, stream=st)
+
+    def step():
+        dev_step()
+        topk_step()
+        merge_step()
+
+    whole = time_steps(step, steps, warmup, stream)
+    parts = {n: time_steps(f, steps, 1, stream)["kern_ms"]
+             for n, f in (("deviation", dev_step), ("topk", topk_step), ("merge", merge_step))}
+    e = 2
+    dev_bytes = T * L * (2 * H * D * e) + T * L * 4
+    topk_bytes = T * L * 4 + n_chunk * L * k * 4
+    merge_bytes = n_chunk * k * L * 2 * (2 * H * D * e)
+    total = dev_bytes + topk_bytes + merge_bytes
+    out = dict(workload="BASELINE config 3: batched selective recompute, 32 req x 6 chunks x 512 "
+                        "tokens, Llama-3-8B KV shape bf16, top-15% (k=77) per chunk",
+               tokens=T, k=k, ms_per_step=whole["step_ms"], tokens_per_s=T / (whole["step_ms"] / 1e3),
+               algorithmic_bytes=total, GBps=_gbps(total, whole["step_ms"]),
+               frac=_gbps(total, whole["step_ms"]) / PEAK_HBM_GBPS,
+               kernels={"deviation": dict(ms=parts["deviation"], bytes=dev_bytes,
+                                          GBps=_gbps(dev_bytes, parts["deviation"])),
+                        "topk": dict(ms=parts["topk"], bytes=topk_bytes),
+                        "merge": dict(ms=parts["merge"], bytes=merge_bytes,
+                                      GBps=_gbps(merge_bytes, parts["merge"]))})
+    del layers, k_new, v_new, keys, sel
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_config4(steps, warmup, seed=0):
+    """KV offload/load: 65536 tokens (4096 pages) of a
+    Llama-3-8B bf16 cache with a seeded random block table. Store: gather the
+    pages into a device staging buffer (one call, 32 jobs), then one
+    hipMemcpyAsync per layer record into pinned host memory on a side stream.
+    Load: the reverse (H2D, then scatter). Device-side and host-link rates are
+    reported separately."""
+    from daric_amd import cache_ops
+    c = CFG4
+    dev = torch.device("cuda:0")
+    L, H, D, PS, NB = c["layers"], c["kv_heads"], c["head_dim"], c["block_size"], c["num_blocks"]
+    T = c["tokens"]
+    n_pages = T // PS
+    g = torch.Generator().manual_seed(seed)
+    ids = (torch.randperm(NB - 1, generator=g)[:n_pages] + 1).to(torch.int32)
+    names = layer_names(L)
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    cache = [torch.randn(2, NB, PS, H, D, generator=gd, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    per_layer = 2 * n_pages * PS * H * D * 2
+    staging = torch.empty(L * per_layer, dtype=torch.uint8, device=dev)
+    host = torch.empty(L * per_layer, dtype=torch.uint8, pin_memory=True)
+    cp = cache_ops.CacheCopier()
+    for n, t in zip(names, cache):
+        cp.register_layer(n, t, False)
+    cp.register_store(staging)
+    flat = torch.cat([ids] * L).to(dev)
+    offs = [i * per_layer for i in range(L)]
+    sizes = [per_layer] * L
+    ioff = [i * n_pages for i in range(L + 1)]
+    stream = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(device=dev)
+
+    gather = time_steps(lambda: cp.gather_pages(names, offs, sizes, flat, ioff, stream.cuda_stream),
+                        steps, warmup, stream)
+    scatter = time_steps(lambda: cp.scatter_pages(names, offs, sizes, flat, ioff, stream.cuda_stream),
+                         steps, warmup, stream)
+
+    def host_copy(d2h):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        side.wait_stream(stream)
+        ev0.record(side)
+        if d2h:
+            cache_ops.batched_memcpy_d2h(staging, host, offs, offs, sizes, side.cuda_stream)
+        else:
+            cache_ops.batched_memcpy_h2d(host, staging, offs, offs, sizes, side.cuda_stream)
+        ev1.record(side)
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1)
+
+    host_copy(True)
+    n_host = max(1, min(steps, 3))
+    d2h_ms = float(np.median([host_copy(True) for _ in range(n_host)]))
+    h2d_ms = float(np.median([host_copy(False) for _ in range(n_host)]))
+    dev_bytes = 2 * L * per_layer
+    link_bytes = L * per_layer
+    out = dict(workload="BASELINE config 4: KV offload/load of 65536 tokens (4096 random pages), "
+                        "Llama-3-8B KV shape bf16",
+               tokens=T,
+               gather=dict(ms=gather["step_ms"], kernel_ms=gather["kern_ms"],
+                           GBps=_gbps(dev_bytes, gather["kern_ms"]),
+                           frac=_gbps(dev_bytes, gather["kern_ms"]) / PEAK_HBM_GBPS),
+               scatter=dict(ms=scatter["step_ms"], kernel_ms=scatter["kern_ms"],
+                            GBps=_gbps(dev_bytes, scatter["kern_ms"]),
+                            frac=_gbps(dev_bytes, scatter["kern_ms"]) / PEAK_HBM_GBPS),
+               device_algorithmic_bytes=dev_bytes,
+               d2h=dict(ms=d2h_ms, GBps=_gbps(link_bytes, d2h_ms)),
+               h2d=dict(ms=h2d_ms, GBps=_gbps(link_bytes, h2d_ms)),
+               host_link_bytes=link_bytes,
+               note="host link: pinned torch memory, one hipMemcpyAsync per layer record on a side stream")
+    del cache, staging, host, cp
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_config5(steps, warmup, seed=0):
+    """fp8 KV cache at Llama-3-70B per-layer KV shape: 80
+    layers x [2, 8193, 16, 8, 128] e4m3 with per-(layer, head) fp32 K scales
+    (amax / 448); 16 chunks x 2048 tokens staged as e4m3 codes of N(0,1)
+    values; one step = scatter_pages_rerotate (dequant -> rotate to offsets
+    0..32767 -> saturating RTNE requant -> scatter, 1280 jobs). The selection
+    at 10% per chunk (k = 205) on the fp8 cache is timed as a second figure."""
+    from daric_amd import cache_ops
+    c = CFG5
+    dev = torch.device("cuda:0")
+    L, H, D, PS, NB = c["layers"], c["kv_heads"], c["head_dim"], c["block_size"], c["num_blocks"]
+    C, CT = c["chunks"], c["chunk_tokens"]
+    T = C * CT
+    g = torch.Generator().manual_seed(seed)
+    ids = (torch.randperm(NB - 1, generator=g)[: T // PS] + 1).to(torch.int32)
+    names = layer_names(L)
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    cache = [torch.zeros(2, NB, PS, H, D, dtype=torch.uint8, device=dev) for _ in range(L)]
+    k_scales = (torch.rand(L, H, generator=gd, device=dev) * 2.0 + 3.0) / 448.0   # amax ~ 3..5 sigma
+    span = PS * H * D
+    job_bytes = 2 * (CT // PS) * span
+    staging = torch.empty(C * L * job_bytes, dtype=torch.uint8, device=dev)
+    piece = 1 << 28
+    for o in range(0, staging.numel(), piece):
+        n = min(piece, staging.numel() - o)
+        vals = torch.randn(n, generator=gd, device=dev) / 0.01      # codes of N(0,1) / (~4/448)
+        staging[o:o + n] = vals.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    del vals
+    cp = cache_ops.CacheCopier()
+    for l, (n, t) in enumerate(zip(names, cache)):
+        cp.register_layer(n, t, False)
+        cp.register_k_scale(n, k_scales[l].contiguous())
+    cp.register_store(staging)
+    jn, offs, sizes, flat, ioff, deltas, ntok = [], [], [], [], [0], [], []
+    off = 0
+    for ci in range(C):
+        bids = ids[ci * (CT // PS):(ci + 1) * (CT // PS)].tolist()
+        for n in names:
+            jn.append(n); offs.append(off); sizes.append(job_bytes); flat.extend(bids)
+            ioff.append(len(flat)); deltas.append(ci * CT); ntok.append(CT)
+            off += job_bytes
+    idx = torch.tensor(flat, dtype=torch.int32, device=dev)
+    inv = (1.0 / (c["rope_theta"] ** (torch.arange(0, D, 2, dtype=torch.float32) / D))).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    fused = time_steps(lambda: cp.scatter_pages_rerotate(jn, offs, sizes, idx, ioff, deltas, ntok, inv, D,
+                                                         True, stream.cuda_stream), steps, warmup, stream)
+    fused_bytes = T * L * 2 * (2 * H * D * 1)
+    # selection on the fp8 cache: recomputed K (bf16) vs the dequantised cached K
+    k = max(1, int(round(c["k_frac"] * CT)))
+    bt = ids.to(dev)
+    chunks = [(ci * (CT // PS), ci * CT, CT, k) for ci in range(C)]
+    k_new = torch.randn(L, T, H, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    keys = torch.empty(L, T, dtype=torch.float32, device=dev)
+    sel = torch.empty(L, C, k, dtype=torch.int32, device=dev)
+
+    def sel_step():
+        cache_ops.kv_deviation(cache, False, bt, k_new, chunks, keys=keys, stream=stream.cuda_stream,
+                               k_scales=k_scales)
+        cache_ops.topk_per_chunk(keys, chunks, kmax=k, out=sel, stream=stream.cuda_stream)
+
+    selection = time_steps(sel_step, steps, warmup, stream)
+    sel_bytes = T * L * H * D * (2 + 1) + 2 * T * L * 4 + C * L * k * 4
+    out = dict(workload="BASELINE config 5: fp8 e4m3 KV at Llama-3-70B per-layer shape, 80 layers, "
+                        "16 chunks x 2048 tokens, dequant->rotate->requant+scatter to offsets 0..32767",
+               tokens=T, ms_per_step=fused["step_ms"], tokens_per_s=T / (fused["step_ms"] / 1e3),
+               kernel_ms=fused["kern_ms"], algorithmic_bytes=fused_bytes,
+               GBps=_gbps(fused_bytes, fused["kern_ms"]),
+               frac=_gbps(fused_bytes, fused["kern_ms"]) / PEAK_HBM_GBPS,
+               selection=dict(k=k, ms_per_step=selection["step_ms"], algorithmic_bytes=sel_bytes,
+                              GBps=_gbps(sel_bytes, selection["step_ms"])))
+    del cache, staging, cp, k_new, keys, sel
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_cpu_baseline(cfg, budget_s=12.0):
     """The CPU oracle's fused scatter + re-rotate over the whole workload (all
     layers, 256 jobs) with a reduced 1024-block pool (same bytes moved): one
@@ -227,6 +476,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--extra", default="3,4,5",
+                    help="other BASELINE configs to measure after the headline (comma list, or 'none')")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (torch copy_) `steps` times, the "
                          "known-size reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -244,6 +495,11 @@ def main():
     tok_s = r["T"] / (r["step_ms"] / 1e3)
     achieved = nbytes / (r["kern_ms"] / 1e3) / 1e9
     g_achieved = nbytes / (r["g_kern_ms"] / 1e3) / 1e9
+    torch.cuda.empty_cache()
+    extra = {}
+    runners = {"3": run_config3, "4": run_config4, "5": run_config5}
+    for cname in [x.strip() for x in a.extra.split(",") if x.strip() and x.strip() != "none"]:
+        extra[f"config{cname}"] = runners[cname](max(3, a.steps // 2), max(1, a.warmup))
     cpu = None if a.no_cpu else run_cpu_baseline(cfg, a.cpu_budget)
     line = {
         "metric": "reused KV tokens/sec (re-rotate+scatter) at Llama-3-8B shape; HBM GB/s",
@@ -269,6 +525,7 @@ def main():
         "gather": {"ms_per_step": r["g_step_ms"], "kernel_ms": r["g_kern_ms"],
                    "GBps": g_achieved, "frac": g_achieved / PEAK_HBM_GBPS,
                    "tokens_per_s": r["T"] / (r["g_step_ms"] / 1e3)},
+        "extra": extra,
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "GBps")},
     }
     print(json.dumps(line))

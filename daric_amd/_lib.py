@@ -15,6 +15,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libdaric_cache_ops.so")
 MAX_DIMS = 8
+ABI_VERSION = 2
 
 DTYPE_CODES = {
     torch.uint8: 0,
@@ -79,7 +80,7 @@ SIGNATURES = {
     "daric_batched_memcpy_h2d": (c_int, [T, T, I64P, I64P, I64P, c_int64, c_uint64]),
     "daric_rerotate_pages": (c_int, [T, c_int64, c_int, T, P(DaricRopeSegment), c_int64, P(DaricRope), T,
                                      c_uint64]),
-    "daric_kv_deviation": (c_int, [T, c_int64, c_int, T, T, P(DaricChunk), c_int64, T, c_uint64]),
+    "daric_kv_deviation": (c_int, [T, c_int64, c_int, T, T, P(DaricChunk), c_int64, T, T, c_uint64]),
     "daric_topk_per_chunk": (c_int, [T, P(DaricChunk), c_int64, T, c_uint64]),
     "daric_merge_rows": (c_int, [T, c_int64, c_int, T, T, T, P(DaricChunk), c_int64, T, c_uint64]),
 }
@@ -100,7 +101,7 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.daric_abi_version() != 1:
+    if lib.daric_abi_version() != ABI_VERSION:
         raise ImportError("daric_amd HIP library ABI version mismatch")
     _lib = lib
     return lib
@@ -116,19 +117,22 @@ def check(status: int) -> None:
 
 
 def desc(t: torch.Tensor) -> DaricTensor:
-    if t.dim() > MAX_DIMS:
-        raise RuntimeError(f"tensor rank {t.dim()} exceeds {MAX_DIMS}")
+    n = t.dim()
+    if n > MAX_DIMS:
+        raise RuntimeError(f"tensor rank {n} exceeds {MAX_DIMS}")
     d = DaricTensor()
     d.data = t.data_ptr()
-    d.ndim = t.dim()
+    d.ndim = n
     d.elem_size = t.element_size()
-    d.device = t.device.index if t.is_cuda else -1
-    if t.is_cuda and d.device is None:
-        d.device = torch.cuda.current_device()
+    dv = t.device
+    if dv.type == "cuda":
+        d.device = dv.index if dv.index is not None else torch.cuda.current_device()
+    else:
+        d.device = -1
     d.dtype = DTYPE_CODES.get(t.dtype, 15)
-    for i, (s, st) in enumerate(zip(t.shape, t.stride())):
-        d.sizes[i] = s
-        d.strides[i] = st
+    if n:
+        d.sizes[:n] = tuple(t.shape)
+        d.strides[:n] = t.stride()
     return d
 
 

@@ -21,6 +21,7 @@ import ctypes
 from collections.abc import Sequence
 from typing import Optional
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -202,10 +203,21 @@ def batched_memcpy_h2d(shm: torch.Tensor, staging: torch.Tensor, shm_offsets: Se
     _memcpy(load().daric_batched_memcpy_h2d, staging, shm, stg_offsets, shm_offsets, sizes, stream, False)
 
 
+_LAYER_ARRAYS: dict = {}
+
+
 def _layer_array(layers: Sequence[torch.Tensor]):
-    arr = (_lib.DaricTensor * max(len(layers), 1))()
-    for i, t in enumerate(layers):
-        arr[i] = desc(t)
+    """daric_tensor array of `layers`, cached per (address, shape, strides,
+    dtype, device) signature: callers pass the same cache tensors every call."""
+    key = tuple((t.data_ptr(), t.shape, t.stride(), t.dtype, t.device) for t in layers)
+    arr = _LAYER_ARRAYS.get(key)
+    if arr is None:
+        arr = (_lib.DaricTensor * max(len(layers), 1))()
+        for i, t in enumerate(layers):
+            arr[i] = desc(t)
+        if len(_LAYER_ARRAYS) >= 64:
+            _LAYER_ARRAYS.clear()
+        _LAYER_ARRAYS[key] = arr
     return arr
 
 
@@ -223,7 +235,8 @@ def rerotate_pages(layers: Sequence[torch.Tensor], page_first: bool, block_table
     dev = layers[0].device
     st = _resolve_stream(stream, dev)
     rope = _rope(inv_freq, rotary_dim, is_neox_style, dev)
-    sarr = (DaricRopeSegment * len(segs))(*[DaricRopeSegment(*(int(x) for x in s)) for s in segs])
+    seg_np = np.ascontiguousarray(np.asarray(segs, dtype=np.int64).reshape(-1, 4))
+    sarr = ctypes.cast(seg_np.ctypes.data, ctypes.POINTER(DaricRopeSegment))
     bt = desc(block_table)
     ks = desc(k_scales) if k_scales is not None else None
     check(load().daric_rerotate_pages(_layer_array(layers), len(layers), 1 if page_first else 0,
@@ -234,27 +247,35 @@ def rerotate_pages(layers: Sequence[torch.Tensor], page_first: bool, block_table
 
 
 def _chunks(chunks):
-    ch = list(chunks)
-    return (DaricChunk * max(len(ch), 1))(*[DaricChunk(*(int(x) for x in c)) for c in ch]), len(ch)
+    """(pointer to daric_chunk[n], n, keep-alive) from a sequence of
+    (bt_offset, row_offset, n_tokens, k) tuples or an int64 [n, 4] array."""
+    a = np.ascontiguousarray(np.asarray(chunks, dtype=np.int64).reshape(-1, 4))
+    if a.shape[0] == 0:
+        a = np.zeros((1, 4), np.int64)
+        return ctypes.cast(a.ctypes.data, ctypes.POINTER(DaricChunk)), 0, a
+    return ctypes.cast(a.ctypes.data, ctypes.POINTER(DaricChunk)), a.shape[0], a
 
 
 def kv_deviation(layers: Sequence[torch.Tensor], page_first: bool, block_table: torch.Tensor,
                  k_new: torch.Tensor, chunks, keys: Optional[torch.Tensor] = None,
-                 stream: int = 0) -> torch.Tensor:
+                 stream: int = 0, k_scales: Optional[torch.Tensor] = None) -> torch.Tensor:
     """keys[l, row] = sum over (h, d) of (k_new - cached K)^2 in the fixed
     order of daric_amd/csrc/select_kernels.hip. chunks: (bt_offset,
-    row_offset, n_tokens, k)."""
+    row_offset, n_tokens, k). k_scales: [L, H] fp32 per-head scales of an fp8
+    cache (None: scale 1)."""
     layers = list(layers)
     dev = layers[0].device
     if keys is None:
         keys = torch.zeros(len(layers), k_new.shape[1], dtype=torch.float32, device=dev)
     st = _resolve_stream(stream, dev)
-    carr, n = _chunks(chunks)
+    carr, n, _keep = _chunks(chunks)
     bt, kn, kd = desc(block_table), desc(k_new), desc(keys)
+    ks = desc(k_scales) if k_scales is not None else None
     check(load().daric_kv_deviation(_layer_array(layers), len(layers), 1 if page_first else 0,
-                                    ctypes.byref(bt), ctypes.byref(kn), carr, n, ctypes.byref(kd),
+                                    ctypes.byref(bt), ctypes.byref(kn), carr, n,
+                                    ctypes.byref(ks) if ks is not None else None, ctypes.byref(kd),
                                     ctypes.c_uint64(st)))
-    _record(st, dev, block_table, k_new, keys)
+    _record(st, dev, block_table, k_new, keys, k_scales)
     return keys
 
 
@@ -268,7 +289,7 @@ def topk_per_chunk(keys: torch.Tensor, chunks, kmax: Optional[int] = None,
     if out is None:
         out = torch.empty(keys.shape[0], len(ch), kmax, dtype=torch.int32, device=keys.device)
     st = _resolve_stream(stream, keys.device)
-    carr, n = _chunks(ch)
+    carr, n, _keep = _chunks(ch)
     kd, od = desc(keys), desc(out)
     check(load().daric_topk_per_chunk(ctypes.byref(kd), carr, n, ctypes.byref(od), ctypes.c_uint64(st)))
     _record(st, keys.device, keys, out)
@@ -282,7 +303,7 @@ def merge_rows(layers: Sequence[torch.Tensor], page_first: bool, block_table: to
     layers = list(layers)
     dev = layers[0].device
     st = _resolve_stream(stream, dev)
-    carr, n = _chunks(chunks)
+    carr, n, _keep = _chunks(chunks)
     bt, kn, si = desc(block_table), desc(k_new), desc(sel_idx)
     vn = desc(v_new) if v_new is not None else None
     check(load().daric_merge_rows(_layer_array(layers), len(layers), 1 if page_first else 0,

@@ -810,8 +810,8 @@ extern "C" {
 
 int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_first,
                        const daric_tensor* block_table, const daric_tensor* k_new,
-                       const daric_chunk* chunks, int64_t n_chunks, daric_tensor* keys,
-                       uint64_t stream) {
+                       const daric_chunk* chunks, int64_t n_chunks, const daric_tensor* k_scales,
+                       daric_tensor* keys, uint64_t stream) {
     return guarded([&] {
         DARIC_CHECK(n_layers > 0 && layers != nullptr, "layers must not be empty");
         for (int64_t i = 0; i < n_layers; ++i) check_tensor_struct(&layers[i], "kv layer");
@@ -830,6 +830,13 @@ int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_fi
         DARIC_CHECK(keys->device == t.device && keys->dtype == DARIC_DTYPE_FLOAT32 && keys->ndim == 2 &&
                     keys->sizes[0] == n_layers && keys->sizes[1] == T && is_contiguous(*keys),
                     "keys must be a contiguous float32 [n_layers, T] tensor");
+        const bool has_scales = k_scales != nullptr && k_scales->data != nullptr;
+        if (has_scales) {
+            DARIC_CHECK(ck == kE4M3, "k_scales apply to fp8 (e4m3) caches only");
+            DARIC_CHECK(k_scales->device == t.device && k_scales->dtype == DARIC_DTYPE_FLOAT32 &&
+                        is_contiguous(*k_scales) && numel(*k_scales) == n_layers * g.H,
+                        "k_scales must be a contiguous float32 [n_layers, H] tensor on the layers' device");
+        }
         const int64_t ces = t.elem_size;
         const int64_t need = ck == kE4M3 ? 8 : 16;
         DARIC_CHECK(g.D % 8 == 0 && (g.sb * ces) % need == 0 && (g.ss * ces) % need == 0 &&
@@ -852,7 +859,9 @@ int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_fi
                          static_cast<const int32_t*>(block_table->data),
                          static_cast<const uint8_t*>(k_new->data), nk, T,
                          static_cast<const SelChunk*>(up.get()), static_cast<int>(c.v.size()),
-                         static_cast<int>(c.tiles), nullptr, static_cast<float*>(keys->data), st);
+                         static_cast<int>(c.tiles),
+                         has_scales ? static_cast<const float*>(k_scales->data) : nullptr,
+                         static_cast<float*>(keys->data), st);
     });
 }
 

@@ -257,7 +257,16 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
 // from LDS into registers once per tile. NeoX pair halves (units k and
 // k +- n_rot of the same row, always in the same wavefront) are exchanged with
 // ds_bpermute. GPT-J pairs are adjacent elements of one unit and need no
-// exchange. Rows that are not rotated are stored as loaded.
+// exchange. Values are converted, rotated and repacked one 32-bit word at a
+// time. Rows that are not rotated are stored as loaded.
+//
+// fp8 (e4m3) with per-head scales: dequantise -> rotate -> requantise is
+// sat_rtne(rot(q * s) / s) with one scale s for both members of a pair (they
+// lie in the same head row), and a rotation is linear, so that equals
+// sat_rtne(rot(q)) up to float32 rounding (relative 2^-24, far below the
+// e4m3 quantum). The kernel therefore rotates the code values directly and
+// saturates on requantisation; the registered scales are needed only where
+// cached values meet other data (kv_deviation).
 #ifndef DARIC_ROT_LANE_UNROLL
 #define DARIC_ROT_LANE_UNROLL 4
 #endif
@@ -267,6 +276,7 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
     const float* __restrict__ inv_freq) {
     using E = Elem<KIND>;
     constexpr int VE = E::VE;
+    constexpr int EPW = E::EPW;
     constexpr int NC = NEOX ? VE : VE / 2;  // cos/sin values per lane
     constexpr int UNR = DARIC_ROT_LANE_UNROLL;
     __shared__ float s_cos[kMaxHalfRot];
@@ -298,7 +308,6 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
     const int pi0 = NEOX ? (first ? k : k - nr) * VE : k * (VE / 2);
     const int n_units = static_cast<int>(j.span / 16);
     const int half = g.R / 2;
-    const float* __restrict__ ksc = j.k_scale;
     const u32x4* __restrict__ src = reinterpret_cast<const u32x4*>(stage);
     u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(cache);
 
@@ -344,29 +353,29 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
                 st_nt(dst + i, v[u]);
                 continue;
             }
-            float scale = 1.0f;
-            if (KIND == kE4M3 && ksc != nullptr) {
-                const int h = g.tok_div == 1
-                    ? static_cast<int>(gd.ps.div(r) - gd.h.div(gd.ps.div(r)) * g.H)
-                    : static_cast<int>(r - gd.h.div(r) * g.H);
-                scale = ksc[h];
-            }
-            float x[VE];
-            E::unpack(v[u], x, scale);
-            if (NEOX) {
-                float y[VE];
-                E::unpack(pv, y, scale);
+            u32x4 out;
 #pragma unroll
-                for (int e = 0; e < VE; ++e) x[e] = x[e] * cs[e] + y[e] * ss[e];
-            } else {
+            for (int w = 0; w < 4; ++w) {
+                float x[EPW];
+                E::unpack_word(v[u][w], x);
+                if (NEOX) {
+                    float y[EPW];
+                    E::unpack_word(pv[w], y);
 #pragma unroll
-                for (int m = 0; m < VE / 2; ++m) {
-                    const float x1 = x[2 * m], x2 = x[2 * m + 1];
-                    x[2 * m] = x1 * cs[m] - x2 * ss[m];
-                    x[2 * m + 1] = x2 * cs[m] + x1 * ss[m];
+                    for (int e = 0; e < EPW; ++e)
+                        x[e] = x[e] * cs[w * EPW + e] + y[e] * ss[w * EPW + e];
+                } else {
+#pragma unroll
+                    for (int m = 0; m < EPW / 2; ++m) {
+                        const int pi = w * (EPW / 2) + m;
+                        const float x1 = x[2 * m], x2 = x[2 * m + 1];
+                        x[2 * m] = x1 * cs[pi] - x2 * ss[pi];
+                        x[2 * m + 1] = x2 * cs[pi] + x1 * ss[pi];
+                    }
                 }
+                out[w] = E::pack_word(x);
             }
-            st_nt(dst + i, E::pack(x, 1.0f / scale));
+            st_nt(dst + i, out);
         }
     }
 }

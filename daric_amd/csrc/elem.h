@@ -98,8 +98,23 @@ enum ElemKind : int { kBF16 = 0, kF16 = 1, kE4M3 = 2 };
 
 template <int KIND> struct Elem;
 
+// Per-32-bit-word forms (EPW elements per word) let a kernel convert, compute
+// and repack one word at a time, which keeps few values live in registers.
 template <> struct Elem<kBF16> {
     static constexpr int VE = 8;  // elements per 16 bytes
+    static constexpr int EPW = 2;
+    __device__ static inline void unpack_word(uint32_t w, float* x) {
+        x[0] = u2f(w << 16);
+        x[1] = u2f(w & 0xffff0000u);
+    }
+    __device__ static inline uint32_t pack_word(const float* x) {
+#ifdef __HIP_DEVICE_COMPILE__
+        const f32x2 p = {x[0], x[1]};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2));
+#else
+        return f32_to_bf16(x[0]) | (f32_to_bf16(x[1]) << 16);
+#endif
+    }
     __device__ static inline void unpack(const u32x4& v, float* x, float) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -127,6 +142,14 @@ template <> struct Elem<kBF16> {
 
 template <> struct Elem<kF16> {
     static constexpr int VE = 8;
+    static constexpr int EPW = 2;
+    __device__ static inline void unpack_word(uint32_t w, float* x) {
+        x[0] = f16_to_f32(w & 0xffffu);
+        x[1] = f16_to_f32(w >> 16);
+    }
+    __device__ static inline uint32_t pack_word(const float* x) {
+        return f32_to_f16(x[0]) | (f32_to_f16(x[1]) << 16);
+    }
     __device__ static inline void unpack(const u32x4& v, float* x, float) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -147,6 +170,23 @@ template <> struct Elem<kF16> {
 // sat_rtne(value * (1 / scale)).
 template <> struct Elem<kE4M3> {
     static constexpr int VE = 16;
+    static constexpr int EPW = 4;
+    __device__ static inline void unpack_word(uint32_t w, float* x) {
+#ifdef DARIC_FP8_SOFTWARE
+#pragma unroll
+        for (int b = 0; b < 4; ++b) x[b] = e4m3_to_f32((w >> (8 * b)) & 0xffu);
+#else
+        e4m3x4_to_f32_hw(w, x);
+#endif
+    }
+    __device__ static inline uint32_t pack_word(const float* x) {
+#ifdef DARIC_FP8_SOFTWARE
+        return f32_to_e4m3(x[0]) | (f32_to_e4m3(x[1]) << 8) | (f32_to_e4m3(x[2]) << 16) |
+               (f32_to_e4m3(x[3]) << 24);
+#else
+        return f32x4_to_e4m3_hw(x);
+#endif
+    }
     __device__ static inline void unpack(const u32x4& v, float* x, float scale) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define DARIC_ABI_VERSION 1
+#define DARIC_ABI_VERSION 2
 
 /* Status codes. */
 #define DARIC_OK 0
@@ -219,11 +219,13 @@ typedef struct daric_chunk {
 /* keys[l, row_offset + j] = sum over (h, d) of (k_new[l, row, h, d] - K_cache)^2
  * in fp32, in the fixed order documented in daric_amd/csrc/select.hip.
  * layers: n_layers paged caches (same geometry); k_new: [n_layers, T, H, D]
- * contiguous, same dtype; keys: [n_layers, T] fp32 contiguous. */
+ * contiguous, bf16 or fp16; keys: [n_layers, T] fp32 contiguous. For an fp8
+ * (e4m3) cache, k_scales is NULL (scale 1) or an [n_layers, H] fp32 device
+ * tensor: cached K is dequantised as float32(code value * scale[l, h]). */
 int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_first,
                        const daric_tensor* block_table, const daric_tensor* k_new,
                        const daric_chunk* chunks, int64_t n_chunks,
-                       daric_tensor* keys, uint64_t stream);
+                       const daric_tensor* k_scales, daric_tensor* keys, uint64_t stream);
 
 /* For every (layer, chunk) select the chunk's k tokens with the largest keys
  * (ties: lower token index first) and write their chunk-local token indices

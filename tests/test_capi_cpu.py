@@ -59,7 +59,7 @@ def test_exports_every_declared_symbol(lib):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover the header"
-    assert lib.daric_abi_version() == 1
+    assert lib.daric_abi_version() == _lib.ABI_VERSION == 2
 
 
 def fake(shape, dtype, device=0, strides=None, ptr=0x10000000):

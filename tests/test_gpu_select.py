@@ -102,3 +102,48 @@ def test_deviation_llama_shape(dev):
                                     k_new.to(dev), chunks)
     torch.cuda.synchronize()
     assert np.array_equal(keys_g.cpu().numpy().view(np.uint32), keys_o.view(np.uint32))
+
+
+@pytest.mark.parametrize("layout", ["nhd", "pf"])
+def test_deviation_fp8_with_scales(dev, layout):
+    """fp8 (e4m3) cache with per-(layer, head) scales: cached K is dequantised
+    as float32(code * scale) before the fixed-order sum (configuration 5's
+    selection on an fp8 cache). Keys and indices bit-exact."""
+    from oracle import fp8 as ofp8
+    g = torch.Generator().manual_seed(11)
+    L, nb, ps, h, d = 2, 40, 16, 4, 64
+    layers = [make_layer(layout, nb, ps, h, d, torch.uint8, g) for _ in range(L)]
+    pf = layers[0][1]
+    cpu = [t for t, _ in layers]
+    scales = (torch.rand(L, h, generator=g) * 0.05 + 0.01).float()
+    perm = np.random.default_rng(11).permutation(np.arange(1, nb)).tolist()
+    chunk_tokens = (200, 97)
+    bt, chunks, p, row = [], [], 0, 0
+    for n in chunk_tokens:
+        npg = -(-n // ps)
+        chunks.append((len(bt), row, n, max(1, int(round(0.1 * n)))))
+        bt.extend(perm[p:p + npg])
+        p += npg
+        row += n
+    bt = np.asarray(bt, np.int32)
+    T = row
+    rng = np.random.default_rng(12)
+    k_new = torch.empty(L, T, h, d, dtype=torch.bfloat16)
+    for l in range(L):
+        kv = osel.k_rows_view(cpu[l], pf)
+        for (bo, ro, n, _k) in chunks:
+            blk, s = osel.chunk_slots(bt, bo, n, ps)
+            codes = kv[torch.as_tensor(blk), torch.as_tensor(s)].numpy()
+            vals = ofp8.decode(codes) * scales[l].numpy()[:, None]
+            noise = 0.01 * rng.standard_t(3, size=vals.shape)
+            k_new[l, ro:ro + n] = torch.from_numpy((vals + noise).astype(np.float32)).to(torch.bfloat16)
+    keys_o = osel.deviation(cpu, pf, bt, k_new, chunks, k_scales=scales.numpy())
+    keys_g = cache_ops.kv_deviation([to_dev(t, dev) for t in cpu], pf, torch.from_numpy(bt).to(dev),
+                                    k_new.to(dev), chunks, k_scales=scales.to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(keys_g.cpu().numpy().view(np.uint32), keys_o.view(np.uint32))
+    kmax = max(c[3] for c in chunks)
+    sel_o = osel.topk_per_chunk(keys_o, chunks, kmax)
+    sel_g = cache_ops.topk_per_chunk(keys_g, chunks, kmax=kmax)
+    torch.cuda.synchronize()
+    assert np.array_equal(sel_g.cpu().numpy(), sel_o)
