@@ -1,0 +1,210 @@
+"""Counterpart of the reference's Adapter (daric/adaption/adapter.py:90-402)
+on the gfx950 kernels: same methods, same arguments, same call sites
+(daric/integration/vllm/worker.py:217, 230-231, 280, 321).
+
+The reference launches one Triton program per (token, head) and one launch
+per layer, after building per-token combined cos/sin tables with torch ops.
+Here every re-rotation request becomes a list of same-shift segments
+(bt_offset, tok_start, n_tokens, delta) over one concatenated block table,
+and one rerotate_pages call covers every layer that shares a cache geometry
+and rotary embedding; cos/sin are formed from the rotary inverse frequencies
+in registers on the GPU.
+
+The layer topology the reference reads from the process-global
+ProcessLocalConfig.cache_topo (configs/engine.py:11-70) is passed to the
+constructor instead (any object with get_all_layer_names(),
+get_group_idx(name) and layers[name].page_first).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import cache_ops
+from .policy import DARICPolicy
+
+__all__ = ["AdaptionConfig", "LayerCacheTopo", "CacheTopo", "Adapter", "plan_load_segments",
+           "plan_multi_segments"]
+
+
+@dataclass
+class AdaptionConfig:
+    """configs/engine.py:164-171."""
+    rerotate: bool
+    recompute: bool
+    recompute_policy: Optional[str]
+    recompute_avg_num: int
+    function: str = "linear"
+    r: float = 0.1
+
+
+@dataclass
+class LayerCacheTopo:
+    """configs/engine.py:11-17 (the fields the adapter reads)."""
+    group_idx: int
+    logical_block_size: int
+    block_byte_size: int
+    page_first: bool
+    is_mamba: bool = False
+
+
+@dataclass
+class CacheTopo:
+    """configs/engine.py:20-35: layers by name, KV-cache groups of layer names."""
+    layers: dict = field(default_factory=dict)
+    groups: list = field(default_factory=list)
+
+    def get_all_layer_names(self) -> list:
+        return sorted(self.layers.keys())
+
+    def get_group_idx(self, layer_name: str) -> int:
+        for g_idx, group in enumerate(self.groups):
+            if layer_name in group:
+                return g_idx
+        raise ValueError(f"Layer {layer_name} not found in any group.")
+
+
+def plan_load_segments(metas, group_idx: int):
+    """apply_rerotate_load's planning (adapter.py:208-265): metas with a
+    non-empty chunk whose saved position differs from ptr[0] move every token
+    by ptr[0] - saved_pos. Returns (block table int32, segments)."""
+    bt: list = []
+    segs = []
+    for meta in metas:
+        old_pos = int(meta.saved_pos)
+        new_pos = int(meta.ptr[0])
+        n = int(meta.ptr[1] - meta.ptr[0])
+        if n <= 0 or old_pos == new_pos:
+            continue
+        blocks = meta.block_ids[group_idx]
+        if isinstance(blocks, torch.Tensor):
+            blocks = blocks.tolist()
+        segs.append((len(bt), 0, n, new_pos - old_pos))
+        bt.extend(int(b) for b in blocks)
+    return np.asarray(bt, dtype=np.int32), segs
+
+
+def plan_multi_segments(group_ptrs, block_ids_list, group_idx: int):
+    """apply_rerotate_multi's planning (adapter.py:127-171): in a request with
+    more than two groups, groups 1..n-2 of non-zero length move by
+    group_ptr[i] - group_ptr[0]; token offsets count from group_ptr[0] in the
+    request's block list."""
+    bt: list = []
+    segs = []
+    for req_idx, group_ptr in enumerate(group_ptrs):
+        n_groups = len(group_ptr) - 1
+        if n_groups <= 2:
+            continue
+        base = group_ptr[0]
+        req_segs = []
+        for i in range(1, n_groups - 1):
+            glen = group_ptr[i + 1] - group_ptr[i]
+            if glen > 0:
+                req_segs.append((group_ptr[i] - base, glen, group_ptr[i] - base))
+        if not req_segs:
+            continue
+        blocks = block_ids_list[req_idx][group_idx]
+        if isinstance(blocks, torch.Tensor):
+            blocks = blocks.tolist()
+        off = len(bt)
+        segs.extend((off, t0, n, d) for t0, n, d in req_segs)
+        bt.extend(int(b) for b in blocks)
+    return np.asarray(bt, dtype=np.int32), segs
+
+
+def _inv_freq(rotary) -> torch.Tensor:
+    """fp32 inverse frequencies of a rotary embedding: an `inv_freq` attribute,
+    else vLLM's RotaryEmbedding._compute_inv_freq(base) (which the llama3 /
+    YaRN subclasses override with their scaled frequencies)."""
+    inv = getattr(rotary, "inv_freq", None)
+    if inv is None and hasattr(rotary, "_compute_inv_freq"):
+        inv = rotary._compute_inv_freq(rotary.base)
+    if inv is None:
+        raise RuntimeError("rotary embedding exposes neither inv_freq nor _compute_inv_freq(base)")
+    return torch.as_tensor(inv).detach().to(torch.float32).reshape(-1)
+
+
+class Adapter:
+    def __init__(self, config: AdaptionConfig, cache_topo=None):
+        self.config = config
+        self.cache_topo = cache_topo if cache_topo is not None else CacheTopo()
+        self.num_layers = len(self.cache_topo.get_all_layer_names())
+        self.kvcaches: dict = {}
+        self.rotary_embeds: dict = {}
+        self._inv_cache: dict = {}
+        if config.recompute_policy == "daric":
+            self.recompute_policy = DARICPolicy(config.recompute_avg_num, function=config.function,
+                                                r=config.r)
+        else:
+            self.recompute_policy = None
+        self.rerotate = config.rerotate
+
+    # ------------------------------------------------------------ registration
+    def register_kvcaches(self, kvcaches: dict) -> None:
+        self.kvcaches = kvcaches
+
+    def register_rotary_embed(self, layer_name: str, rotary_embed) -> None:
+        if layer_name not in self.rotary_embeds:
+            self.rotary_embeds[layer_name] = rotary_embed
+
+    def register_done(self) -> bool:
+        return len(self.rotary_embeds) == self.num_layers
+
+    # ------------------------------------------------------------ rotation
+    def _device_inv_freq(self, rotary, device) -> torch.Tensor:
+        key = (id(rotary), str(device))
+        hit = self._inv_cache.get(key)
+        if hit is None or hit[0] is not rotary:
+            hit = (rotary, _inv_freq(rotary).to(device).contiguous())
+            self._inv_cache[key] = hit
+        return hit[1]
+
+    def _rotate(self, layer_names: Sequence[str], plan) -> None:
+        """Runs `plan(group_idx) -> (block table, segments)` for every KV-cache
+        group and rotates the group's layers, batching the layers that share a
+        geometry and a rotary embedding into one call."""
+        by_group: dict = {}
+        for name in layer_names:
+            if name in self.kvcaches:
+                by_group.setdefault(self.cache_topo.get_group_idx(name), []).append(name)
+        for group_idx, names in by_group.items():
+            bt, segs = plan(group_idx)
+            if not segs:
+                continue
+            first = self.kvcaches[names[0]]
+            device = first.device
+            bt_dev = torch.from_numpy(bt).to(device, non_blocking=True)
+            batches: dict = {}
+            for name in names:
+                kv = self.kvcaches[name]
+                rotary = self.rotary_embeds[name]
+                page_first = bool(self.cache_topo.layers[name].page_first)
+                key = (tuple(kv.shape), kv.stride(), kv.dtype, page_first, id(rotary),
+                       int(rotary.rotary_dim), bool(rotary.is_neox_style))
+                batches.setdefault(key, (rotary, page_first, []))[2].append(kv)
+            for rotary, page_first, kvs in batches.values():
+                cache_ops.rerotate_pages(kvs, page_first, bt_dev, segs,
+                                         self._device_inv_freq(rotary, device),
+                                         int(rotary.rotary_dim), bool(rotary.is_neox_style))
+
+    def apply_rerotate_multi(self, group_ptrs: List[List[int]], block_ids_list) -> None:
+        if not self.rerotate:
+            return
+        assert len(group_ptrs) == len(block_ids_list)
+        self._rotate(list(self.kvcaches.keys()),
+                     lambda g: plan_multi_segments(group_ptrs, block_ids_list, g))
+
+    def apply_rerotate_load(self, metas, layer_name: Optional[str] = None) -> None:
+        if not self.rerotate:
+            return
+        names = [layer_name] if layer_name is not None else list(self.kvcaches.keys())
+        self._rotate(names, lambda g: plan_load_segments(metas, g))
+
+    # ------------------------------------------------------------ recompute
+    def get_recompute_length(self, group_ptr: List[int]) -> List[int]:
+        if self.recompute_policy is None:
+            return []
+        return self.recompute_policy.get_recompute_ptrs(group_ptr)

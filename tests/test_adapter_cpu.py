@@ -1,0 +1,108 @@
+"""Adapter counterpart, host side: segment planning against the oracle's
+restatement of apply_rerotate_load/multi (reference adapter.py:118-295),
+layer batching by group and geometry, the rerotate/recompute switches."""
+import numpy as np
+import pytest
+import torch
+
+from daric_amd import adapter as ad
+from daric_amd.policy import DARICPolicy
+from oracle import rope as orope
+from tests.adapter_fakes import FakeMeta, FakeRotary
+
+
+def test_load_planning_matches_oracle():
+    rng = np.random.default_rng(3)
+    metas, raw = [], []
+    pos = 0
+    for i in range(12):
+        n = int(rng.integers(0, 70))
+        saved = int(rng.choice([pos, 0, 5, pos + 3]))
+        blocks = rng.permutation(np.arange(1, 400))[: -(-n // 16) or 1].tolist()
+        metas.append(FakeMeta(f"c{i}", [pos, pos + n], saved, (blocks, [b + 1000 for b in blocks])))
+        raw.append((pos, pos + n, saved, blocks))
+        pos += n
+    bt, segs = ad.plan_load_segments(metas, 0)
+    obt, osegs = orope.load_segments(raw)
+    assert bt.tolist() == obt.tolist() and segs == osegs
+    bt1, segs1 = ad.plan_load_segments(metas, 1)     # second KV-cache group: its own block lists
+    assert bt1.tolist() == [b + 1000 for b in obt.tolist()] and segs1 == osegs
+
+
+def test_multi_planning_matches_oracle():
+    ptrs = [[10, 20, 30, 45, 50], [0, 5, 9], [0, 16, 16, 40, 64, 80]]
+    blocks = [([1, 2, 3, 4],), ([9],), ([5, 6, 7, 8, 11],)]
+    bt, segs = ad.plan_multi_segments(ptrs, blocks, 0)
+    obt, osegs = orope.multi_segments(ptrs, [b[0] for b in blocks])
+    assert bt.tolist() == obt.tolist() and segs == osegs
+
+
+class Recorder:
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, layers, page_first, block_table, segments, inv_freq, rotary_dim,
+                 is_neox_style=True, k_scales=None, stream=0):
+        self.calls.append(dict(n_layers=len(layers), page_first=page_first,
+                               bt=block_table.tolist(), segs=list(segments),
+                               inv=inv_freq.tolist(), R=rotary_dim, neox=is_neox_style))
+
+
+def make_adapter(rerotate=True, policy="daric"):
+    names = [f"model.layers.{i}.self_attn.attn" for i in range(4)]
+    topo = ad.CacheTopo(layers={n: ad.LayerCacheTopo(0 if i < 3 else 1, 16, 1, False)
+                                for i, n in enumerate(names)},
+                        groups=[names[:3], names[3:]])
+    cfg = ad.AdaptionConfig(rerotate=rerotate, recompute=True, recompute_policy=policy,
+                            recompute_avg_num=32, function="linear", r=0.5)
+    a = ad.Adapter(cfg, topo)
+    kv = {n: torch.zeros(2, 8, 16, 2, 32, dtype=torch.bfloat16) for n in names}
+    kv[names[2]] = torch.zeros(2, 8, 16, 2, 64, dtype=torch.bfloat16)   # different geometry
+    a.register_kvcaches(kv)
+    rot = FakeRotary(32)
+    for n in names:
+        a.register_rotary_embed(n, rot)
+    return a, names
+
+
+def test_batching_by_group_and_geometry(monkeypatch):
+    rec = Recorder()
+    monkeypatch.setattr(ad.cache_ops, "rerotate_pages", rec)
+    a, names = make_adapter()
+    assert a.register_done()
+    metas = [FakeMeta("a", [0, 20], 100, ([3, 4], [7, 8])), FakeMeta("b", [20, 30], 20, ([5], [9]))]
+    a.apply_rerotate_load(metas)
+    # group 0: two geometries -> two calls; group 1: one call; meta "b" is not moved
+    assert sorted(c["n_layers"] for c in rec.calls) == [1, 1, 2]
+    for c in rec.calls:
+        assert c["segs"] == [(0, 0, 20, -100)]
+        assert c["bt"] in ([3, 4], [7, 8])
+        assert c["R"] == 32 and c["neox"] and not c["page_first"]
+        np.testing.assert_allclose(c["inv"], FakeRotary(32)._compute_inv_freq(500000.0).numpy())
+    rec.calls.clear()
+    a.apply_rerotate_load(metas, layer_name=names[3])          # layerwise load
+    assert len(rec.calls) == 1 and rec.calls[0]["bt"] == [7, 8]
+
+
+def test_switches(monkeypatch):
+    rec = Recorder()
+    monkeypatch.setattr(ad.cache_ops, "rerotate_pages", rec)
+    a, _ = make_adapter(rerotate=False, policy=None)
+    a.apply_rerotate_load([FakeMeta("a", [0, 20], 100, ([3, 4], [7, 8]))])
+    a.apply_rerotate_multi([[0, 10, 20, 30]], [([1, 2], [3, 4])])
+    assert rec.calls == [] and a.get_recompute_length([0, 10, 20]) == []
+    b, _ = make_adapter()
+    ptr = [0, 256, 512, 768, 1024]
+    assert b.get_recompute_length(ptr) == DARICPolicy(32, 0.5, "linear").get_recompute_ptrs(ptr)
+    b.apply_rerotate_multi([[0, 10, 20]], [([1, 2], [3, 4])])   # two groups: nothing moves
+    assert rec.calls == []
+
+
+def test_inv_freq_source():
+    r = FakeRotary(64)
+    np.testing.assert_array_equal(ad._inv_freq(r).numpy(), r._compute_inv_freq(r.base).numpy())
+
+    class Bare:
+        rotary_dim, is_neox_style = 8, True
+    with pytest.raises(RuntimeError, match="inv_freq"):
+        ad._inv_freq(Bare())

@@ -92,3 +92,25 @@ def test_deviation_uses_slots():
         cached = layer[0, bt[j // ps], j % ps].double()
         ref = ((k_new[0, j].double() - cached) ** 2).sum().item()
         assert abs(keys[0, j] - ref) <= 1e-5 * ref
+
+
+def test_deviation_fp8_dequantises_with_per_head_scale():
+    """fp8 cache: cached K is code value x scale[layer, head] (float64 check,
+    independent of the fixed order); no scales means scale 1."""
+    from oracle import fp8
+    rng = np.random.default_rng(4)
+    nb, ps, h, d = 6, 4, 3, 16
+    codes = fp8.encode(rng.standard_normal(2 * nb * ps * h * d).astype(np.float32))
+    layer = torch.from_numpy(codes).view(2, nb, ps, h, d)
+    bt = np.array([5, 2], np.int32)
+    k_new = torch.randn(1, 8, h, d).to(torch.bfloat16)
+    scales = np.array([[0.5, 0.031, 2.0]], np.float32)
+    keys = select.deviation([layer], False, bt, k_new, [(0, 0, 8, 2)], k_scales=scales)
+    keys1 = select.deviation([layer], False, bt, k_new, [(0, 0, 8, 2)])
+    for j in range(8):
+        q = fp8.decode(layer[0, bt[j // ps], j % ps].numpy()).astype(np.float64)
+        kn = k_new[0, j].double().numpy()
+        ref = ((kn - q * scales[0][:, None].astype(np.float64)) ** 2).sum()
+        ref1 = ((kn - q) ** 2).sum()
+        assert abs(keys[0, j] - ref) <= 1e-5 * ref
+        assert abs(keys1[0, j] - ref1) <= 1e-5 * ref1
