@@ -1,0 +1,257 @@
+"""Store/load of reused KV chunks between a GPU's paged cache and pinned host
+records: the per-GPU part of the daric-store's GPU I/O (reference
+daric/management/service/gpu_kv_io.py:130-205 RankIPCContext, :318-409 copy
+plan and record header, :424-584 _do_store/_do_load) on the gfx950 kernels.
+
+Record format (byte-compatible with the reference): for each meta, the
+gather_pages bytes of every layer in registration order (the reference
+registers layers in sorted name order, configs/engine.py:25-27), followed by a
+4096-byte header whose first 8 bytes hold the little-endian int64 saved
+position.
+
+Pipeline: the reference gathers a batch into one staging buffer, copies it to
+host, and only then gathers the next batch, with a full stream synchronisation
+per load chunk. Here staging is split into two halves: the copy kernels run on
+the compute stream and the host DMA on a copy stream, so batch b+1's
+gather (scatter) overlaps batch b's device-to-host (host-to-device) copy; events
+order each half's reuse. Both streams keep the default priority. Batching keeps
+the reference's limits: at most MAX_BATCH_SIZE metas and one staging half of
+bytes per batch on store; load chunks bounded by the staging half.
+
+The host buffer must be page-locked memory (torch pin_memory or hipHostMalloc)
+so the DMA engines can reach it.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import cache_ops
+
+__all__ = ["POSITION_SIZE", "REGISTRATION_CHUNK_BYTES", "KVIOContext", "split_registration_copies",
+           "build_copy_plan", "per_meta_cache_size"]
+
+POSITION_SIZE = 4096
+INT64_SIZE = 8
+REGISTRATION_CHUNK_BYTES = 1 << 30
+DEFAULT_STAGING_BYTES = 256 << 20
+
+
+def split_registration_copies(stg_offsets, shm_offsets, sizes, chunk_bytes=REGISTRATION_CHUNK_BYTES):
+    """Cuts each (staging, host, size) region where the host offset crosses a
+    multiple of chunk_bytes (the reference registers host memory in 1 GiB
+    pieces and never lets one copy span two, gpu_kv_io.py:110-127)."""
+    if not (len(stg_offsets) == len(shm_offsets) == len(sizes)):
+        raise ValueError("Copy offsets and sizes must have the same length.")
+    if chunk_bytes <= 0:
+        raise ValueError("Registration chunk size must be positive.")
+    rs, rh, rn = [], [], []
+    for s, h, n in zip(stg_offsets, shm_offsets, sizes):
+        if s < 0 or h < 0 or n < 0:
+            raise ValueError("Copy offsets and sizes must be non-negative.")
+        while n > 0:
+            take = min(n, chunk_bytes - h % chunk_bytes)
+            rs.append(s)
+            rh.append(h)
+            rn.append(take)
+            s += take
+            h += take
+            n -= take
+    return rs, rh, rn
+
+
+def per_meta_cache_size(layer_names, group_idxs, layer_bpbs, block_ids_list, layer_name=None):
+    """Cache bytes of each meta's record (header excluded)."""
+    if layer_name is not None:
+        li = layer_names.index(layer_name)
+        return [layer_bpbs[li] * len(b[group_idxs[li]]) for b in block_ids_list]
+    return [sum(bpb * len(b[g]) for g, bpb in zip(group_idxs, layer_bpbs)) for b in block_ids_list]
+
+
+def build_copy_plan(layer_names, group_idxs, layer_bpbs, offsets, block_ids_list, layer_name=None):
+    """Jobs of a batch of metas: (flat int32 block ids, job offsets, indices
+    offsets, job layer names, job sizes), one job per (meta, layer)."""
+    flat: list = []
+    ioff = [0]
+    job_off, job_sz, job_names = [], [], []
+    if layer_name is not None:
+        li = layer_names.index(layer_name)
+        sel = [(li, layer_name)]
+    else:
+        sel = list(enumerate(layer_names))
+    for base, blocks in zip(offsets, block_ids_list):
+        run = 0
+        for li, name in sel:
+            ids = blocks[group_idxs[li]]
+            if isinstance(ids, torch.Tensor):
+                ids = ids.tolist()
+            flat.extend(int(x) for x in ids)
+            ioff.append(len(flat))
+            nbytes = layer_bpbs[li] * len(ids)
+            job_off.append(base + run)
+            job_sz.append(nbytes)
+            job_names.append(name)
+            run += nbytes
+    return np.asarray(flat, dtype=np.int32), job_off, ioff, job_names, job_sz
+
+
+class KVIOContext:
+    """One GPU's store/load context: a write copier (gathers into staging) and
+    a read copier (scatters from staging), two staging halves, a compute
+    stream and a copy stream."""
+
+    MAX_BATCH_SIZE = 4
+
+    def __init__(self, layer_names: Sequence[str], group_idxs: Sequence[int],
+                 layer_bpbs: Sequence[int], page_firsts: Sequence[bool],
+                 kv_caches: dict, host: torch.Tensor, staging_bytes: int = DEFAULT_STAGING_BYTES,
+                 device: Optional[torch.device] = None):
+        if host.dtype != torch.uint8 or host.dim() != 1 or host.is_cuda:
+            raise ValueError("host records must be a 1-D uint8 CPU tensor")
+        if not host.is_pinned():
+            raise ValueError("host records must be page-locked (pin_memory=True)")
+        self.layer_names = list(layer_names)
+        self.group_idxs = list(group_idxs)
+        self.layer_bpbs = list(layer_bpbs)
+        self.page_firsts = list(page_firsts)
+        first = kv_caches[self.layer_names[0]]
+        self.device = device if device is not None else first.device
+        self.host = host
+        self.half = int(staging_bytes) // 2 // 256 * 256
+        if self.half <= 0:
+            raise ValueError("staging_bytes too small")
+        self.staging = torch.empty(2 * self.half, dtype=torch.uint8, device=self.device)
+        self.compute = torch.cuda.Stream(device=self.device)
+        self.copy = torch.cuda.Stream(device=self.device)
+        self.write_copier = cache_ops.CacheCopier()
+        self.read_copier = cache_ops.CacheCopier()
+        for name, pf in zip(self.layer_names, self.page_firsts):
+            self.write_copier.register_layer(name, kv_caches[name], bool(pf))
+            self.read_copier.register_layer(name, kv_caches[name], bool(pf))
+        self.write_copier.register_store(self.staging)
+        self.read_copier.register_store(self.staging)
+        self._half_free = [None, None]   # event after which a staging half may be overwritten
+
+    # ------------------------------------------------------------ helpers
+    def cache_sizes(self, block_ids_list, layer_name=None) -> List[int]:
+        return per_meta_cache_size(self.layer_names, self.group_idxs, self.layer_bpbs,
+                                   block_ids_list, layer_name)
+
+    def record_size(self, block_ids, layer_name=None) -> int:
+        """Bytes a record of one meta occupies in host memory (header included)."""
+        return self.cache_sizes([block_ids], layer_name)[0] + POSITION_SIZE
+
+    def _write_positions(self, position_offsets, saved_positions):
+        host = self.host.numpy()
+        for off, pos in zip(position_offsets, saved_positions):
+            host[off: off + POSITION_SIZE] = 0
+            host[off: off + INT64_SIZE] = np.frombuffer(np.int64(pos).tobytes(), np.uint8)
+
+    def read_positions(self, position_offsets) -> List[int]:
+        host = self.host.numpy()
+        return [int(host[o: o + INT64_SIZE].view(np.int64)[0]) for o in position_offsets]
+
+    def _batches(self, sizes, cap, max_count):
+        i, n = 0, len(sizes)
+        while i < n:
+            j, acc = i, 0
+            while j < n and j - i < max_count and acc + sizes[j] <= cap:
+                acc += sizes[j]
+                j += 1
+            if j == i:
+                raise RuntimeError(f"KV IO: single meta is {sizes[i]} bytes, larger than the "
+                                   f"{cap}-byte staging half; raise staging_bytes")
+            yield i, j
+            i = j
+
+    # ------------------------------------------------------------ store
+    def store(self, offsets: Sequence[int], block_ids_list, saved_positions: Sequence[int],
+              layer_name: Optional[str] = None, wait_stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Writes one record per meta at host offset offsets[i] (the reference's
+        _do_store after allocation). Returns once the records, headers included,
+        are in host memory."""
+        offsets = [int(o) for o in offsets]
+        sizes = self.cache_sizes(block_ids_list, layer_name)
+        if wait_stream is not None:
+            self.compute.wait_stream(wait_stream)
+        per_meta = 1 if layer_name is not None else len(self.layer_names)
+        b = 0
+        for i, j in self._batches(sizes, self.half, self.MAX_BATCH_SIZE):
+            h = b % 2
+            base = h * self.half
+            flat, host_off, ioff, names, job_sz = build_copy_plan(
+                self.layer_names, self.group_idxs, self.layer_bpbs, offsets[i:j],
+                block_ids_list[i:j], layer_name)
+            stg = np.cumsum([0] + job_sz[:-1]).astype(np.int64) + base
+            if self._half_free[h] is not None:
+                self.compute.wait_event(self._half_free[h])
+            with torch.cuda.stream(self.compute):
+                idx = torch.from_numpy(flat).to(self.device, non_blocking=False)
+            self.write_copier.gather_pages(names, stg.tolist(), job_sz, idx, ioff,
+                                           self.compute.cuda_stream)
+            done = torch.cuda.Event()
+            done.record(self.compute)
+            self.copy.wait_event(done)
+            meta_stg = [int(stg[k * per_meta]) for k in range(j - i)]
+            cs, ch, cn = split_registration_copies(meta_stg, offsets[i:j], sizes[i:j])
+            cache_ops.batched_memcpy_d2h(self.staging, self.host, cs, ch, cn, self.copy.cuda_stream)
+            ev = torch.cuda.Event()
+            ev.record(self.copy)
+            self._half_free[h] = ev
+            b += 1
+        self.copy.synchronize()
+        self._write_positions([o + s for o, s in zip(offsets, sizes)], saved_positions)
+
+    # ------------------------------------------------------------ load
+    def load(self, offsets: Sequence[int], block_ids_list, layer_name: Optional[str] = None,
+             wait_stream: Optional[torch.cuda.Stream] = None, rerotate=None) -> List[int]:
+        """Scatters each meta's record back into the paged cache (the
+        reference's _do_load) and returns the saved positions. With
+        rerotate = (new_positions, num_tokens, inv_freq, rotary_dim, is_neox),
+        the K rows of each meta's first num_tokens[i] tokens are moved from the
+        saved position to new_positions[i] in the same pass
+        (scatter_pages_rerotate); the saved positions are read from the headers
+        first, which live in host memory. Device work is left queued on the
+        compute stream; the returned event marks its end."""
+        offsets = [int(o) for o in offsets]
+        sizes = self.cache_sizes(block_ids_list, layer_name)
+        saved = self.read_positions([o + s for o, s in zip(offsets, sizes)])
+        if wait_stream is not None:
+            self.copy.wait_stream(wait_stream)
+        per_meta = 1 if layer_name is not None else len(self.layer_names)
+        b = 0
+        for i, j in self._batches(sizes, self.half, 1 << 30):
+            h = b % 2
+            base = h * self.half
+            flat, host_off, ioff, names, job_sz = build_copy_plan(
+                self.layer_names, self.group_idxs, self.layer_bpbs, offsets[i:j],
+                block_ids_list[i:j], layer_name)
+            stg = np.cumsum([0] + job_sz[:-1]).astype(np.int64) + base
+            if self._half_free[h] is not None:
+                self.copy.wait_event(self._half_free[h])
+            meta_stg = [int(stg[k * per_meta]) for k in range(j - i)]
+            cs, ch, cn = split_registration_copies(meta_stg, offsets[i:j], sizes[i:j])
+            cache_ops.batched_memcpy_h2d(self.host, self.staging, ch, cs, cn, self.copy.cuda_stream)
+            arrived = torch.cuda.Event()
+            arrived.record(self.copy)
+            self.compute.wait_event(arrived)
+            with torch.cuda.stream(self.compute):
+                idx = torch.from_numpy(flat).to(self.device, non_blocking=False)
+            if rerotate is None:
+                self.read_copier.scatter_pages(names, stg.tolist(), job_sz, idx, ioff,
+                                               self.compute.cuda_stream)
+            else:
+                new_pos, ntok, inv, rdim, neox = rerotate
+                deltas = [int(new_pos[k]) - int(saved[k]) for k in range(i, j) for _ in range(per_meta)]
+                nt = [int(ntok[k]) for k in range(i, j) for _ in range(per_meta)]
+                self.read_copier.scatter_pages_rerotate(names, stg.tolist(), job_sz, idx, ioff, deltas,
+                                                        nt, inv, rdim, neox, self.compute.cuda_stream)
+            ev = torch.cuda.Event()
+            ev.record(self.compute)
+            self._half_free[h] = ev
+            b += 1
+        self.done = torch.cuda.Event()
+        self.done.record(self.compute)
+        return saved

@@ -1,0 +1,135 @@
+"""Store/load pipeline (daric_amd.kv_io.KVIOContext) against the oracle's
+restatement of the daric-store GPU I/O (oracle/kvio.py): host record bytes
+and headers bit-exact after store, cache bytes bit-exact after load, the
+fused re-rotating load within the rotation bar; small staging halves force
+multi-batch pipelining and reuse of both halves."""
+import numpy as np
+import pytest
+import torch
+
+from daric_amd import kv_io
+from oracle import kvio as okv
+from oracle import rope as orope
+from tests.gpu_util import assert_rotation_parity, make_layer, rotation_region, same_bytes, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def setup(dev, n_layers=3, nb=64, layout="nhd", dtype=torch.bfloat16, two_groups=False, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    names = sorted(f"model.layers.{i}.self_attn.attn" for i in range(n_layers))
+    cpu, pf = {}, False
+    for n in names:
+        cpu[n], pf = make_layer(layout, nb, 16, 4, 64, dtype, g)
+    t0 = cpu[names[0]]
+    from oracle.layout import page_copy_shape
+    s = page_copy_shape(tuple(t0.shape), tuple(t0.stride()), t0.element_size(), pf)
+    bpb = [s.prefix_size * s.suffix_size] * n_layers
+    groups = [i % 2 if two_groups else 0 for i in range(n_layers)]
+    return names, cpu, pf, bpb, groups
+
+
+def metas_blocks(rng, n_meta, nb, two_groups):
+    """Per meta 1-5 block ids per group, disjoint across metas (no null block)."""
+    p0 = rng.permutation(np.arange(1, nb)).tolist()
+    p1 = rng.permutation(np.arange(1, nb)).tolist()
+    out = []
+    for _ in range(n_meta):
+        k0, k1 = int(rng.integers(1, 6)), int(rng.integers(1, 6))
+        g0, p0 = p0[:k0], p0[k0:]
+        g1, p1 = p1[:k1], p1[k1:]
+        out.append((g0, g1) if two_groups else (g0,))
+    return out
+
+
+def record_offsets(ctx, blocks, gap=4096 + 256):
+    offs, o = [], 8192
+    for b in blocks:
+        offs.append(o)
+        o += ctx.record_size(b) + gap
+    return offs, o
+
+
+@pytest.mark.parametrize("two_groups,staging", [(False, 1 << 20), (True, 600 << 10)])
+def test_store_then_load_matches_oracle(dev, two_groups, staging):
+    names, cpu, pf, bpb, groups = setup(dev, two_groups=two_groups)
+    rng = np.random.default_rng(1)
+    blocks = metas_blocks(rng, 7, 64, two_groups)
+    dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
+    host_size = 64 << 20
+    host = torch.zeros(host_size, dtype=torch.uint8, pin_memory=True)
+    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * len(names), dev_caches, host, staging_bytes=staging)
+    offs, end = record_offsets(ctx, blocks)
+    assert end < host_size
+    saved = [int(x) for x in rng.integers(0, 1 << 40, len(blocks))]
+    ctx.store(offs, blocks, saved)
+    shm = torch.zeros(host_size, dtype=torch.uint8)
+    okv.OracleKVIO(names, groups, bpb, [pf] * len(names), cpu, shm).store(offs, blocks, saved)
+    assert torch.equal(host, shm), "host records differ from the oracle's"
+    # load into zeroed caches
+    fresh_cpu = {n: torch.zeros_like(t) for n, t in cpu.items()}
+    fresh_dev = {n: to_dev(t, dev) for n, t in fresh_cpu.items()}
+    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * len(names), fresh_dev, host, staging_bytes=staging)
+    got = ctx2.load(offs, blocks)
+    torch.cuda.synchronize()
+    want = okv.OracleKVIO(names, groups, bpb, [pf] * len(names), fresh_cpu, shm).load(offs, blocks)
+    assert got == want == saved
+    for n in names:
+        assert same_bytes(fresh_dev[n], fresh_cpu[n])
+
+
+def test_layerwise_and_null_blocks(dev):
+    names, cpu, pf, bpb, groups = setup(dev, layout="pf")
+    rng = np.random.default_rng(2)
+    blocks = metas_blocks(rng, 3, 64, False)
+    host = torch.zeros(8 << 20, dtype=torch.uint8, pin_memory=True)
+    shm = torch.zeros(8 << 20, dtype=torch.uint8)
+    dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
+    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, dev_caches, host, staging_bytes=1 << 20)
+    offs = [4096 + i * (1 << 20) for i in range(3)]
+    ctx.store(offs, blocks, [5, 6, 7], layer_name=names[1])
+    okv.OracleKVIO(names, groups, bpb, [pf] * 3, cpu, shm).store(offs, blocks, [5, 6, 7], layer_name=names[1])
+    assert torch.equal(host, shm)
+    # load with a null block (id 0) in the list: that page is neither read nor written
+    blocks0 = [([0] + b[0][1:],) for b in blocks]
+    fresh_cpu = {n: torch.full_like(t, 7) for n, t in cpu.items()}
+    fresh_dev = {n: to_dev(t, dev) for n, t in fresh_cpu.items()}
+    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, fresh_dev, host, staging_bytes=1 << 20)
+    assert ctx2.load(offs, blocks0, layer_name=names[1]) == [5, 6, 7]
+    torch.cuda.synchronize()
+    okv.OracleKVIO(names, groups, bpb, [pf] * 3, fresh_cpu, shm).load(offs, blocks0, layer_name=names[1])
+    for n in names:
+        assert same_bytes(fresh_dev[n], fresh_cpu[n])
+
+
+def test_load_rerotate_matches_oracle(dev):
+    names, cpu, pf, bpb, groups = setup(dev)
+    rng = np.random.default_rng(3)
+    blocks = metas_blocks(rng, 5, 64, False)
+    host = torch.zeros(32 << 20, dtype=torch.uint8, pin_memory=True)
+    shm = torch.zeros(32 << 20, dtype=torch.uint8)
+    dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
+    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, dev_caches, host, staging_bytes=640 << 10)
+    offs, _ = record_offsets(ctx, blocks)
+    saved = [0, 512, 77, 3000, 9]
+    ctx.store(offs, blocks, saved)
+    okv.OracleKVIO(names, groups, bpb, [pf] * 3, cpu, shm).store(offs, blocks, saved)
+    assert torch.equal(host, shm)
+    R = 64
+    inv = orope.default_inv_freq(R, 500000.0)
+    new_pos = [100, 512, 4000, 0, 20000]
+    ntok = [len(b[0]) * 16 - 3 for b in blocks]
+    fresh_cpu = {n: torch.zeros_like(t) for n, t in cpu.items()}
+    fresh_dev = {n: to_dev(t, dev) for n, t in fresh_cpu.items()}
+    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, fresh_dev, host, staging_bytes=640 << 10)
+    ctx2.load(offs, blocks, rerotate=(new_pos, ntok, torch.from_numpy(inv).to(dev), R, True))
+    torch.cuda.synchronize()
+    okv.OracleKVIO(names, groups, bpb, [pf] * 3, fresh_cpu, shm).load(
+        offs, blocks, rerotate=(new_pos, ntok, inv, R, True))
+    slots = []
+    for b, nt, np_, sp in zip(blocks, ntok, new_pos, saved):
+        if np_ != sp:
+            slots += [b[0][j // 16] * 16 + j % 16 for j in range(nt)]
+    for n in names:
+        mask, pn = rotation_region(fresh_cpu[n], pf, R, slots, True)
+        assert_rotation_parity(fresh_dev[n], fresh_cpu[n], mask, pn)
