@@ -7,12 +7,15 @@
 // flight per lane, loads before stores. Staging-side loads and cache-side
 // stores are nontemporal: every byte is touched once.
 //
-// Block order (measured on MI355X at the Llama-3-8B shape, 256 jobs of
-// 64 pages): the scatter direction runs job-minor -- consecutive workgroups
-// take the same tile of consecutive jobs -- which sustained ~6.3 TB/s against
-// ~6.0 TB/s for a tile-major order; the gather direction runs tile-major within
-// a job and cuts each tile into parts of ~8 KiB, which sustained ~6.3 TB/s
-// against ~5.7 TB/s for whole-tile workgroups.
+// Block order (measured on MI355X at the Llama-3-8B shape): both directions
+// cut each tile into parts of ~8 KiB. The scatter direction runs job-minor --
+// consecutive workgroups take the same part of consecutive jobs -- which
+// sustained ~6.3 TB/s against ~6.0 TB/s for a tile-major order (256 jobs of
+// 64 pages) and 5.9 against 5.3-5.4 TB/s (32 jobs of 4096 pages); the gather
+// direction runs tile-major within a job, which sustained ~6.3 TB/s (256 x 64)
+// and 5.8-6.0 TB/s (32 x 4096), against 5.5-5.6 TB/s for whole-tile
+// workgroups and job-minor orders. The fused scatter + rotation runs job-minor
+// on whole tiles.
 //
 // Pages whose block id is 0 (vLLM's null block) are skipped, as the
 // reference's kernels skip them (csrc/cache_ops/kernels.cu:26,39,69,79,104,117);
@@ -393,26 +396,28 @@ constexpr int kMaxY = 65535;
 
 void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int64_t max_span, int vw,
                        bool gather, hipStream_t stream) {
-    if (!gather) {
-        // job-minor: slices of jobs so that max_tiles * slice fits grid.x
-        const int slice = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(n_jobs, kMaxBlocksX / max_tiles)));
-        for (int j0 = 0; j0 < n_jobs; j0 += slice) {
-            const int nj = std::min(slice, n_jobs - j0);
-            const FastDiv fd(static_cast<uint32_t>(nj));
-            const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(max_tiles) * nj));
-            const CopyJob* jp = d_jobs + j0;
-            if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, false, true>), grid, kThreads, 0, stream, jp, fd, 0);
-            else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, false, true>), grid, kThreads, 0, stream, jp, fd, 0);
-            else DARIC_LAUNCH((copy_pages_kernel<1, false, true>), grid, kThreads, 0, stream, jp, fd, 0);
-            check_launch("scatter_pages");
-        }
-        return;
-    }
-    // tile-major within a job, tiles cut into parts of about 8 KiB
+    // tiles cut into parts of about 8 KiB
     int log2_parts = 0;
     while (log2_parts < 3 && (max_span >> (log2_parts + 1)) >= 8192 &&
            (static_cast<int64_t>(max_tiles) << (log2_parts + 1)) <= kMaxBlocksX)
         ++log2_parts;
+    if (!gather) {
+        // job-minor: slices of jobs so that the grid fits grid.x
+        const int64_t units = static_cast<int64_t>(max_tiles) << log2_parts;
+        const int slice = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(n_jobs, kMaxBlocksX / units)));
+        for (int j0 = 0; j0 < n_jobs; j0 += slice) {
+            const int nj = std::min(slice, n_jobs - j0);
+            const FastDiv fd(static_cast<uint32_t>(nj));
+            const dim3 grid(static_cast<unsigned>(units * nj));
+            const CopyJob* jp = d_jobs + j0;
+            if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, false, true>), grid, kThreads, 0, stream, jp, fd, log2_parts);
+            else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, false, true>), grid, kThreads, 0, stream, jp, fd, log2_parts);
+            else DARIC_LAUNCH((copy_pages_kernel<1, false, true>), grid, kThreads, 0, stream, jp, fd, log2_parts);
+            check_launch("scatter_pages");
+        }
+        return;
+    }
+    // gather: tile-major within a job
     const FastDiv fd(1);
     for (int j0 = 0; j0 < n_jobs; j0 += kMaxY) {
         const int nj = std::min(kMaxY, n_jobs - j0);
