@@ -286,6 +286,70 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(
     }
 }
 
+// Row merge for 16-byte-aligned rows of at most 4 KiB: each wavefront moves
+// whole token rows -- the K and V rows of kRowTok selected tokens -- with one
+// selection / block-table lookup per token, all loads issued before the
+// stores. Measured on MI355X at configuration 3 (77 of 512 tokens per chunk,
+// 2 KiB rows) it ran ~7% faster than the per-unit merge_kernel.
+constexpr int kRowTok = 2;
+constexpr int kRowUnits = 4;   // 16-byte units per lane per row (rows <= 4 KiB)
+
+__global__ __launch_bounds__(kThreads) void merge_rows_kernel(
+    uint8_t* const* __restrict__ layers, KVGeom g, int es, const int32_t* __restrict__ bt,
+    const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T,
+    const SelChunk* __restrict__ chunks, int n_chunks, const int32_t* __restrict__ sel, int kmax,
+    FastDiv d_upr) {
+    const int l = static_cast<int>(blockIdx.z);
+    const int ci = static_cast<int>(blockIdx.y);
+    const SelChunk& c = chunks[ci];
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int q0 = (static_cast<int>(blockIdx.x) * kWaves + wave) * kRowTok;
+    const int32_t* srow = sel + (static_cast<int64_t>(l) * n_chunks + ci) * kmax;
+    uint8_t* __restrict__ base = layers[l];
+    const int upr = static_cast<int>(d_upr.d);     // 16-byte units per head row
+    const int units = g.H * upr;                   // per K (or V) token row
+    const int64_t rowbytes = static_cast<int64_t>(g.H) * g.D * es;
+    const int qmax = min(kmax, c.k);
+    u32x4 v[kRowTok][2][kRowUnits];
+    uint8_t* dst[kRowTok][2][kRowUnits];
+#pragma unroll
+    for (int t = 0; t < kRowTok; ++t) {
+        const int q = q0 + t;
+        int j = -1, blk = -1;
+        if (q < qmax) {
+            j = srow[q];
+            if (j >= 0 && j < c.n_tokens) blk = bt[c.bt_offset + j / g.PS];
+        }
+        const bool ok = blk > 0 && blk < g.num_blocks;
+#pragma unroll
+        for (int kv = 0; kv < 2; ++kv) {
+#pragma unroll
+            for (int r = 0; r < kRowUnits; ++r) {
+                dst[t][kv][r] = nullptr;
+                const int u = lane + r * 64;
+                if (!ok || u >= units || (kv == 1 && g.v_off < 0)) continue;
+                const int h = static_cast<int>(d_upr.div(static_cast<uint32_t>(u)));
+                const int un = u - h * upr;
+                const int64_t de = static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(j % g.PS) * g.ss +
+                                   static_cast<int64_t>(h) * g.sh + (kv ? g.v_off : 0);
+                const uint8_t* src = (kv ? v_new : k_new) +
+                                     (static_cast<int64_t>(l) * T + c.row_offset + j) * rowbytes +
+                                     static_cast<int64_t>(u) * 16;
+                dst[t][kv][r] = base + de * es + static_cast<int64_t>(un) * 16;
+                v[t][kv][r] = *reinterpret_cast<const u32x4*>(src);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kRowTok; ++t)
+#pragma unroll
+        for (int kv = 0; kv < 2; ++kv)
+#pragma unroll
+            for (int r = 0; r < kRowUnits; ++r)
+                if (dst[t][kv][r] != nullptr) *reinterpret_cast<u32x4*>(dst[t][kv][r]) = v[t][kv][r];
+}
+
 }  // namespace
 
 void launch_deviation(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int cache_kind,
@@ -324,7 +388,13 @@ void launch_merge(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int e
     const bool vec = (g.D * elem_size) % 16 == 0 && (g.sb * elem_size) % 16 == 0 &&
                      (g.ss * elem_size) % 16 == 0 && (g.sh * elem_size) % 16 == 0 &&
                      (g.v_off < 0 || (g.v_off * elem_size) % 16 == 0);
-    if (vec)
+    const int upr = vec ? g.D * elem_size / 16 : 0;
+    if (vec && g.H * upr <= 64 * kRowUnits) {
+        const dim3 rgrid(static_cast<unsigned>((kmax + kWaves * kRowTok - 1) / (kWaves * kRowTok)),
+                         static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
+        DARIC_LAUNCH((merge_rows_kernel), rgrid, kThreads, 0, stream, d_layers, g, elem_size, block_table,
+                     k_new, v_new, T, d_chunks, n_chunks, sel_idx, kmax, FastDiv(static_cast<uint32_t>(upr)));
+    } else if (vec)
         DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d_layers, g, elem_size, block_table, k_new,
                                                         v_new, T, d_chunks, n_chunks, sel_idx, kmax);
     else
