@@ -38,29 +38,41 @@ __device__ __forceinline__ int find_chunk(const SelChunk* __restrict__ ch, int n
     return lo;
 }
 
-// 8 elements starting at p (16 bytes for 2-byte types, 8 bytes for fp8).
+// 8 elements: 16 bytes for 2-byte types, 8 bytes for fp8. Loaded raw (so a
+// lane keeps few registers per load in flight) and converted when summed.
+template <int KIND> struct Raw8 { u32x4 w; };
+template <> struct Raw8<kE4M3> { u32x2 w; };
+
 template <int KIND>
-__device__ __forceinline__ void load8(const uint8_t* p, float* x, float scale) {
-    if (KIND == kE4M3) {
-        const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+__device__ __forceinline__ Raw8<KIND> load_raw8(const uint8_t* p) {
+    Raw8<KIND> r;
+    if constexpr (KIND == kE4M3)
+        r.w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    else
+        r.w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return r;
+}
+
+template <int KIND>
+__device__ __forceinline__ void unpack8(const Raw8<KIND>& r, float* x, float scale) {
+    if constexpr (KIND == kE4M3) {
 #ifdef DARIC_FP8_SOFTWARE
 #pragma unroll
-        for (int b = 0; b < 4; ++b) { x[b] = e4m3_to_f32((w[0] >> (8 * b)) & 0xffu); x[4 + b] = e4m3_to_f32((w[1] >> (8 * b)) & 0xffu); }
+        for (int b = 0; b < 4; ++b) { x[b] = e4m3_to_f32((r.w[0] >> (8 * b)) & 0xffu); x[4 + b] = e4m3_to_f32((r.w[1] >> (8 * b)) & 0xffu); }
 #else
-        e4m3x4_to_f32_hw(w[0], x);
-        e4m3x4_to_f32_hw(w[1], x + 4);
+        e4m3x4_to_f32_hw(r.w[0], x);
+        e4m3x4_to_f32_hw(r.w[1], x + 4);
 #endif
 #pragma unroll
         for (int i = 0; i < 8; ++i) x[i] = x[i] * scale;
     } else {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(p);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             if (KIND == kBF16) {
-                x[2 * q] = u2f(w[q] << 16);
-                x[2 * q + 1] = u2f(w[q] & 0xffff0000u);
+                x[2 * q] = u2f(r.w[q] << 16);
+                x[2 * q + 1] = u2f(r.w[q] & 0xffff0000u);
             } else {
-                const uint32_t word = w[q];
+                const uint32_t word = r.w[q];
                 x[2 * q] = f16_to_f32(word & 0xffffu);
                 x[2 * q + 1] = f16_to_f32(word >> 16);
             }
@@ -111,19 +123,23 @@ __global__ __launch_bounds__(kThreads) void deviation_kernel(
         const int h = e0 / g.D;
         const int d0 = e0 - h * g.D;
         const float scale = (CK == kE4M3 && ksc) ? ksc[h] : 1.0f;
-        float a[kTokPerWave][8], b[kTokPerWave][8];
+        Raw8<NK> ra[kTokPerWave];
+        Raw8<CK> rb[kTokPerWave];
 #pragma unroll
         for (int i = 0; i < kTokPerWave; ++i) {
             if (!valid[i]) continue;
-            load8<NK>(new_row[i] + static_cast<int64_t>(e0) * 2, a[i], 1.0f);
-            load8<CK>(base + (cache_row[i] + static_cast<int64_t>(h) * g.sh + d0) * CES, b[i], scale);
+            ra[i] = load_raw8<NK>(new_row[i] + static_cast<int64_t>(e0) * 2);
+            rb[i] = load_raw8<CK>(base + (cache_row[i] + static_cast<int64_t>(h) * g.sh + d0) * CES);
         }
 #pragma unroll
         for (int i = 0; i < kTokPerWave; ++i) {
             if (!valid[i]) continue;
+            float a[8], b[8];
+            unpack8<NK>(ra[i], a, 1.0f);
+            unpack8<CK>(rb[i], b, scale);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float d = a[i][e] - b[i][e];
+                const float d = a[e] - b[e];
                 const float sq = d * d;
                 acc[i] = acc[i] + sq;
             }
