@@ -102,6 +102,8 @@ public:
 private:
     DescRing() = default;
     static constexpr int kSlots = 16;
+    static constexpr size_t kInitialCap = 1 << 20;
+    bool initialised_ = false;
     int next_ = 0;
     Slot slots_[kSlots];
     std::mutex mu_;

@@ -100,15 +100,29 @@ void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* s
         lk.lock();
     }
     next_ = (idx + 1) % kSlots;
+    // All slots get kInitialCap bytes at the ring's first use: growing a slot
+    // later frees device memory (hipFree waits for the device), which would
+    // stall a call in the middle of a pipelined stream of calls. 1 MiB holds
+    // the descriptors of ~13000 copy jobs.
+    if (!initialised_) {
+        for (Slot& t : slots_) {
+            if (t.ev == nullptr) DARIC_HIP_CHECK(hipEventCreateWithFlags(&t.ev, hipEventDisableTiming));
+            if (t.cap == 0) {
+                DARIC_HIP_CHECK(hipHostMalloc(&t.host, kInitialCap, hipHostMallocCoherent));
+                DARIC_HIP_CHECK(hipMalloc(&t.dev, kInitialCap));
+                t.cap = kInitialCap;
+            }
+        }
+        initialised_ = true;
+    }
     Slot& s = slots_[idx];
     s.in_use = true;
     if (s.pending) {
         DARIC_HIP_CHECK(hipEventSynchronize(s.ev));
         s.pending = false;
     }
-    if (s.ev == nullptr) DARIC_HIP_CHECK(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
     if (bytes > s.cap) {
-        size_t cap = 4096;
+        size_t cap = s.cap * 2;
         while (cap < bytes) cap *= 2;
         if (s.host) DARIC_HIP_CHECK(hipHostFree(s.host));
         if (s.dev) DARIC_HIP_CHECK(hipFree(s.dev));
@@ -129,7 +143,7 @@ void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* s
         // hipMemcpyAsync (a copy-engine transfer the compute queue must then
         // wait for, ~17 us per call in a back-to-back pipeline on MI355X) it
         // stays on the compute queue (~3 us). Slots are 16-byte multiples
-        // of at least 4096 bytes, so the rounded copy stays in bounds.
+        // of at least 1 MiB, so the rounded copy stays in bounds.
         launch_upload(s.host, s.dev, (bytes + 15) / 16, stream);
     } catch (...) {
         s.in_use = false;
