@@ -12,7 +12,12 @@ function on the path, each citing the reference file:line it follows:
   fp8.py     OCP e4m3 encode/decode used by the fp8 path
   select.py  deviation keys, per-chunk top-k and merge (spec of the selection
              kernels; the reference has no such kernel)
-  policy.py  DARICPolicy recompute budget (daric/adaption/policy.py)
+  kvio.py    store/load record format and copy plan of the daric-store GPU I/O
+             (daric/management/service/gpu_kv_io.py)
+
+The recompute budget (daric/adaption/policy.py) is host logic of the product
+(daric_amd/policy.py) and is pinned by vectors of the reference's own function
+(tests/golden/policy_vectors.json), not restated here.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
 this package, and only as the checker or as the timed CPU baseline. The
