@@ -263,6 +263,7 @@ ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_j
     DARIC_CHECK(c->has_store, "store buffer not registered; call register_store() first");
     if (n_jobs == 0) return r;
     DARIC_CHECK(n_jobs > 0 && names != nullptr, "layer_names must not be empty");
+    DARIC_CHECK(n_jobs <= kIntMax, "too many jobs in one call: ", n_jobs);
     validate_common_job_inputs(n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices_offsets,
                                n_indices_offsets, indices);
     const int64_t store_size = numel(c->store);
