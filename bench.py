@@ -153,8 +153,24 @@ def run_gpu(cfg, steps, warmup):
         gcp.gather_pages(w["names"], g_off, g_sizes, g_flat, g_ioff, stream.cuda_stream)
 
     gather = time_steps(gstep, steps, warmup, stream)
+
+    # the worker-side form: in-place re-rotation of the same 8 chunks in all
+    # 32 layers (rerotate_pages, the Adapter's call; K rotated part only)
+    CT = cfg["chunk_tokens"]
+    pages = CT // cfg["block_size"]
+    segs = [(c * pages, 0, CT, c * CT) for c in range(cfg["chunks"]) if c > 0]
+    bt_all = w["ids"].to(dev)
+
+    def rstep():
+        cache_ops.rerotate_pages(w["cache"], False, bt_all, segs, inv, cfg["head_dim"], True,
+                                 stream=stream.cuda_stream)
+
+    inplace = time_steps(rstep, steps, warmup, stream)
+    inplace_bytes = sum(s[2] for s in segs) * L * cfg["kv_heads"] * cfg["head_dim"] * 2 * 2
     return dict(step_ms=fused["step_ms"], wall_s=fused["wall_s"], kern_ms=fused["kern_ms"],
-                g_step_ms=gather["step_ms"], g_kern_ms=gather["kern_ms"], T=T, L=L)
+                g_step_ms=gather["step_ms"], g_kern_ms=gather["kern_ms"], T=T, L=L,
+                r_step_ms=inplace["step_ms"], r_kern_ms=inplace["kern_ms"], r_bytes=inplace_bytes,
+                r_tokens=sum(s[2] for s in segs))
 
 
 # ---------------------------------------------------------------------------
@@ -557,6 +573,13 @@ def main():
         "gather": {"ms_per_step": r["g_step_ms"], "kernel_ms": r["g_kern_ms"],
                    "GBps": g_achieved, "frac": g_achieved / PEAK_HBM_GBPS,
                    "tokens_per_s": r["T"] / (r["g_step_ms"] / 1e3)},
+        "rerotate_inplace": {"ms_per_step": r["r_step_ms"], "kernel_ms": r["r_kern_ms"],
+                             "algorithmic_bytes": r["r_bytes"],
+                             "GBps": _gbps(r["r_bytes"], r["r_kern_ms"]),
+                             "frac": _gbps(r["r_bytes"], r["r_kern_ms"]) / PEAK_HBM_GBPS,
+                             "tokens_per_s": r["r_tokens"] / (r["r_step_ms"] / 1e3),
+                             "note": "rerotate_pages of chunks 1..7 (chunk 0 does not move) in all "
+                                     "layers: K rotated elements read and written"},
         "extra": extra,
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "GBps")},
     }
