@@ -227,7 +227,10 @@ def rerotate_pages(layers: Sequence[torch.Tensor], page_first: bool, block_table
                    k_scales: Optional[torch.Tensor] = None, stream: int = 0) -> None:
     """In-place re-rotation of the K rows of every segment
     (bt_offset, tok_start, n_tokens, delta) in every layer: the counterpart of
-    the reference's per-layer _launch_triton_rerotate (adapter.py:297-396)."""
+    the reference's per-layer _launch_triton_rerotate (adapter.py:297-396).
+    k_scales ([L, H] fp32, positive) is checked but leaves the result
+    unchanged: fp8 codes are rotated as stored, since a per-head scale cancels
+    in a linear rotation (the reference's kernel rotates the raw fp8 values)."""
     layers = list(layers)
     segs = list(segments)
     if not layers or not segs:

@@ -699,7 +699,9 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
         g.num_blocks = static_cast<int32_t>(L.num_blocks);
         g.n_rot = static_cast<int32_t>(vec ? (neox ? half / VE : rope->rotary_dim / VE) : half);
         const int64_t per_tok = L.H * g.n_rot;
-        g.tile_tokens = static_cast<int32_t>(std::max<int64_t>(1, 2048 / std::max<int64_t>(per_tok, 1)));
+        // about 1024 items (vector path) or 2048 pairs (element path) per tile
+        const int64_t tile_items = vec ? 1024 : 2048;
+        g.tile_tokens = static_cast<int32_t>(std::max<int64_t>(1, tile_items / std::max<int64_t>(per_tok, 1)));
 
         std::vector<RopeSeg> segs;
         int64_t tiles = 0;
@@ -738,7 +740,6 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
         launch_rerotate_inplace(d_layers, static_cast<int>(n_layers), g, d_segs,
                                 static_cast<int>(segs.size()), static_cast<int>(tiles),
                                 static_cast<const int32_t*>(block_table->data), rope->inv_freq,
-                                k_scales && k_scales->data ? static_cast<const float*>(k_scales->data) : nullptr,
                                 kind, neox, vec, st);
     });
 }

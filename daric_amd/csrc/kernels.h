@@ -46,12 +46,12 @@ void launch_scatter_rotate(const CopyJob* d_jobs, int n_jobs, int max_tiles,
 
 // In-place K re-rotation over segments of tokens. `layers` is a device array
 // of n_layers K base pointers; `vec` selects 16-byte (true) or per-element
-// (false) access.
+// (false) access. fp8 codes are rotated as stored (a per-head scale cancels
+// in a linear rotation).
 void launch_rerotate_inplace(uint8_t* const* d_layers, int n_layers, const InplaceGeom& g,
                              const RopeSeg* d_segs, int n_segs, int n_tiles,
-                             const int32_t* block_table, const float* inv_freq,
-                             const float* k_scales, int kind, bool neox, bool vec,
-                             hipStream_t stream);
+                             const int32_t* block_table, const float* inv_freq, int kind,
+                             bool neox, bool vec, hipStream_t stream);
 
 // Selection kernels.
 void launch_deviation(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int cache_kind,

@@ -20,7 +20,7 @@ namespace daric {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kVecUnroll = 2;
 constexpr int kMaxHalfRot = 256;
 
 __device__ __forceinline__ int find_segment(const RopeSeg* __restrict__ segs, int n, int tile) {
@@ -43,11 +43,18 @@ __device__ __forceinline__ void fill_cos_sin(float* s_cos, float* s_sin, int hal
     __syncthreads();
 }
 
+// One item = one 16-byte unit of a head row's rotated part (NeoX: a unit of
+// the first half and its partner rotary_dim/2 elements on). Each thread
+// issues its first kVecUnroll items' loads before the cos/sin table is
+// filled, so the loads are in flight while sincosf runs.
+//
+// fp8 codes are rotated as they are stored: the rotation is linear, so a
+// positive per-head scale s gives rot(q * s) / s = rot(q) and cancels.
 template <int KIND, bool NEOX>
 __global__ __launch_bounds__(kThreads) void rerotate_vec_kernel(
     uint8_t* const* __restrict__ layers, InplaceGeom g, const RopeSeg* __restrict__ segs,
     int n_segs, const int32_t* __restrict__ bt, const float* __restrict__ inv_freq,
-    const float* __restrict__ k_scales) {
+    FastDiv d_tok, FastDiv d_rot, FastDiv d_ps) {
     using E = Elem<KIND>;
     constexpr int VE = E::VE;
     constexpr int ES = KIND == kE4M3 ? 1 : 2;
@@ -60,49 +67,47 @@ __global__ __launch_bounds__(kThreads) void rerotate_vec_kernel(
     const int n_tok = min(g.tile_tokens, sg.n_tokens - tok0);
     if (n_tok <= 0 || sg.delta == 0.0f) return;
     const int half = g.R / 2;
-    fill_cos_sin(s_cos, s_sin, half, sg.delta, inv_freq);
 
     uint8_t* __restrict__ base = layers[blockIdx.y];
-    const float* ksc = k_scales ? k_scales + static_cast<int64_t>(blockIdx.y) * g.H : nullptr;
     const int per_tok = g.H * g.n_rot;
     const int items = n_tok * per_tok;
-    const int64_t partner_b = NEOX ? static_cast<int64_t>(half) * ES : 0;
+    const int partner = NEOX ? half * ES / 16 : 0;      // in 16-byte units
+    const uint32_t pos0 = static_cast<uint32_t>(sg.tok_start + tok0);
 
-    for (int b0 = 0; b0 < items; b0 += kThreads * kUnroll) {
-        u32x4 a[kUnroll], bb[kUnroll];
-        int64_t off[kUnroll];
-        int kk[kUnroll], hh[kUnroll];
-        bool ok[kUnroll];
+    for (int b0 = 0; b0 < items; b0 += kThreads * kVecUnroll) {
+        u32x4 a[kVecUnroll], bb[kVecUnroll];
+        u32x4* p[kVecUnroll];
+        int kk[kVecUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < kVecUnroll; ++u) {
             const int it = b0 + u * kThreads + static_cast<int>(threadIdx.x);
-            const int t = it / per_tok;
-            const int rem = it - t * per_tok;
-            const int h = rem / g.n_rot;
-            const int k = rem - h * g.n_rot;
-            const int pos = sg.tok_start + tok0 + t;
-            int blk = -1;
-            if (it < items) blk = bt[sg.bt_offset + pos / g.PS];
-            ok[u] = it < items && blk >= 0 && blk < g.num_blocks;
-            kk[u] = k;
-            hh[u] = h;
-            off[u] = (static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(pos % g.PS) * g.ss +
-                      static_cast<int64_t>(h) * g.sh + static_cast<int64_t>(k) * VE) * ES;
-            if (ok[u]) {
-                a[u] = *reinterpret_cast<const u32x4*>(base + off[u]);
-                if (NEOX) bb[u] = *reinterpret_cast<const u32x4*>(base + off[u] + partner_b);
-            }
+            p[u] = nullptr;
+            kk[u] = 0;
+            if (it >= items) continue;
+            const uint32_t t = d_tok.div(static_cast<uint32_t>(it));
+            const uint32_t rem = static_cast<uint32_t>(it) - t * static_cast<uint32_t>(per_tok);
+            const uint32_t h = d_rot.div(rem);
+            const uint32_t pos = pos0 + t;
+            const uint32_t q = d_ps.div(pos);
+            const int blk = bt[sg.bt_offset + q];
+            if (blk < 0 || blk >= g.num_blocks) continue;
+            kk[u] = static_cast<int>(rem - h * static_cast<uint32_t>(g.n_rot));
+            p[u] = reinterpret_cast<u32x4*>(
+                       base + (static_cast<int64_t>(blk) * g.sb +
+                               static_cast<int64_t>(pos - q * static_cast<uint32_t>(g.PS)) * g.ss +
+                               static_cast<int64_t>(h) * g.sh) * ES) + kk[u];
+            a[u] = *p[u];
+            if (NEOX) bb[u] = p[u][partner];
         }
+        if (b0 == 0) fill_cos_sin(s_cos, s_sin, half, sg.delta, inv_freq);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            if (!ok[u]) continue;
-            const float scale = (KIND == kE4M3 && ksc) ? ksc[hh[u]] : 1.0f;
-            const float inv = 1.0f / scale;
+        for (int u = 0; u < kVecUnroll; ++u) {
+            if (!p[u]) continue;
             float x[VE];
-            E::unpack(a[u], x, scale);
+            E::unpack(a[u], x, 1.0f);
             if (NEOX) {
                 float y[VE];
-                E::unpack(bb[u], y, scale);
+                E::unpack(bb[u], y, 1.0f);
                 const int i0 = kk[u] * VE;
 #pragma unroll
                 for (int e = 0; e < VE; ++e) {
@@ -111,8 +116,8 @@ __global__ __launch_bounds__(kThreads) void rerotate_vec_kernel(
                     x[e] = x1 * c - x2 * sn;
                     y[e] = x2 * c + x1 * sn;
                 }
-                *reinterpret_cast<u32x4*>(base + off[u]) = E::pack(x, inv);
-                *reinterpret_cast<u32x4*>(base + off[u] + partner_b) = E::pack(y, inv);
+                *p[u] = E::pack(x, 1.0f);
+                p[u][partner] = E::pack(y, 1.0f);
             } else {
                 const int i0 = kk[u] * (VE / 2);
 #pragma unroll
@@ -122,32 +127,32 @@ __global__ __launch_bounds__(kThreads) void rerotate_vec_kernel(
                     x[2 * m] = x1 * c - x2 * sn;
                     x[2 * m + 1] = x2 * c + x1 * sn;
                 }
-                *reinterpret_cast<u32x4*>(base + off[u]) = E::pack(x, inv);
+                *p[u] = E::pack(x, 1.0f);
             }
         }
     }
 }
 
 // Per-element variant for layouts whose rows or pair halves are not 16-byte
-// aligned. One item = one rotation pair.
+// aligned. One item = one rotation pair; fp8 codes are rotated as stored, as
+// in the vector kernel.
 template <int KIND>
-__device__ __forceinline__ float load_elem(const uint8_t* p, float scale) {
+__device__ __forceinline__ float load_elem(const uint8_t* p) {
     if (KIND == kBF16) return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
     if (KIND == kF16) return f16_to_f32(*reinterpret_cast<const uint16_t*>(p));
-    return e4m3_to_f32(*p) * scale;
+    return e4m3_to_f32(*p);
 }
 template <int KIND>
-__device__ __forceinline__ void store_elem(uint8_t* p, float v, float inv) {
+__device__ __forceinline__ void store_elem(uint8_t* p, float v) {
     if (KIND == kBF16) *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(f32_to_bf16(v));
     else if (KIND == kF16) *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(f32_to_f16(v));
-    else *p = static_cast<uint8_t>(f32_to_e4m3(v * inv));
+    else *p = static_cast<uint8_t>(f32_to_e4m3(v));
 }
 
 template <int KIND, bool NEOX>
 __global__ __launch_bounds__(kThreads) void rerotate_elem_kernel(
     uint8_t* const* __restrict__ layers, InplaceGeom g, const RopeSeg* __restrict__ segs,
-    int n_segs, const int32_t* __restrict__ bt, const float* __restrict__ inv_freq,
-    const float* __restrict__ k_scales) {
+    int n_segs, const int32_t* __restrict__ bt, const float* __restrict__ inv_freq) {
     constexpr int ES = KIND == kE4M3 ? 1 : 2;
     __shared__ float s_cos[kMaxHalfRot];
     __shared__ float s_sin[kMaxHalfRot];
@@ -159,7 +164,6 @@ __global__ __launch_bounds__(kThreads) void rerotate_elem_kernel(
     const int half = g.R / 2;
     fill_cos_sin(s_cos, s_sin, half, sg.delta, inv_freq);
     uint8_t* __restrict__ base = layers[blockIdx.y];
-    const float* ksc = k_scales ? k_scales + static_cast<int64_t>(blockIdx.y) * g.H : nullptr;
     const int per_tok = g.H * half;
     const int items = n_tok * per_tok;
     for (int it = threadIdx.x; it < items; it += kThreads) {
@@ -174,12 +178,11 @@ __global__ __launch_bounds__(kThreads) void rerotate_elem_kernel(
                             static_cast<int64_t>(pos % g.PS) * g.ss + static_cast<int64_t>(h) * g.sh;
         const int64_t e1 = NEOX ? row + i : row + 2 * i;
         const int64_t e2 = NEOX ? row + i + half : row + 2 * i + 1;
-        const float scale = (KIND == kE4M3 && ksc) ? ksc[h] : 1.0f;
-        const float x1 = load_elem<KIND>(base + e1 * ES, scale);
-        const float x2 = load_elem<KIND>(base + e2 * ES, scale);
+        const float x1 = load_elem<KIND>(base + e1 * ES);
+        const float x2 = load_elem<KIND>(base + e2 * ES);
         const float c = s_cos[i], sn = s_sin[i];
-        store_elem<KIND>(base + e1 * ES, x1 * c - x2 * sn, 1.0f / scale);
-        store_elem<KIND>(base + e2 * ES, x2 * c + x1 * sn, 1.0f / scale);
+        store_elem<KIND>(base + e1 * ES, x1 * c - x2 * sn);
+        store_elem<KIND>(base + e2 * ES, x2 * c + x1 * sn);
     }
 }
 
@@ -187,17 +190,17 @@ __global__ __launch_bounds__(kThreads) void rerotate_elem_kernel(
 
 void launch_rerotate_inplace(uint8_t* const* d_layers, int n_layers, const InplaceGeom& g,
                              const RopeSeg* d_segs, int n_segs, int n_tiles,
-                             const int32_t* block_table, const float* inv_freq,
-                             const float* k_scales, int kind, bool neox, bool vec,
-                             hipStream_t stream) {
+                             const int32_t* block_table, const float* inv_freq, int kind,
+                             bool neox, bool vec, hipStream_t stream) {
     constexpr int kMaxY = 65535;
+    const FastDiv d_tok(static_cast<uint32_t>(g.H * g.n_rot)), d_rot(static_cast<uint32_t>(g.n_rot)),
+        d_ps(static_cast<uint32_t>(g.PS));
     for (int l0 = 0; l0 < n_layers; l0 += kMaxY) {
         const int nl = n_layers - l0 < kMaxY ? n_layers - l0 : kMaxY;
         const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(nl));
         uint8_t* const* lp = d_layers + l0;
-        const float* ks = k_scales ? k_scales + static_cast<int64_t>(l0) * g.H : nullptr;
-#define DARIC_RV(K, N) DARIC_LAUNCH((rerotate_vec_kernel<K, N>), grid, kThreads, 0, stream, lp, g, d_segs, n_segs, block_table, inv_freq, ks)
-#define DARIC_RE(K, N) DARIC_LAUNCH((rerotate_elem_kernel<K, N>), grid, kThreads, 0, stream, lp, g, d_segs, n_segs, block_table, inv_freq, ks)
+#define DARIC_RV(K, N) DARIC_LAUNCH((rerotate_vec_kernel<K, N>), grid, kThreads, 0, stream, lp, g, d_segs, n_segs, block_table, inv_freq, d_tok, d_rot, d_ps)
+#define DARIC_RE(K, N) DARIC_LAUNCH((rerotate_elem_kernel<K, N>), grid, kThreads, 0, stream, lp, g, d_segs, n_segs, block_table, inv_freq)
         if (vec) {
             if (kind == kBF16) { if (neox) DARIC_RV(kBF16, true); else DARIC_RV(kBF16, false); }
             else if (kind == kF16) { if (neox) DARIC_RV(kF16, true); else DARIC_RV(kF16, false); }

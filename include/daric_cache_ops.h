@@ -192,7 +192,10 @@ typedef struct daric_rope_segment {
 /* Rotate, in place, the K rows of every listed token in every layer of
  * `layers` (all with the same shape, strides and dtype; page_first as in
  * reference adapter.py:311-368). `k_scales` is NULL or an [n_layers, H] fp32
- * device tensor of per-head scales for fp8 layers. `block_table` is a 1-D
+ * device tensor of positive per-head scales for fp8 layers; it is checked but
+ * does not change the result: the rotation is linear, so the stored codes are
+ * rotated directly (rot(q * s) / s = rot(q)), as the reference's kernel
+ * rotates the raw fp8 values (adapter.py:30-88). `block_table` is a 1-D
  * contiguous int32 device tensor. */
 int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers, int page_first,
                          const daric_tensor* block_table,
