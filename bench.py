@@ -15,8 +15,8 @@ random block table. One step = one CacheCopier.scatter_pages_rerotate call
 Prints one JSON line. `value` = reused KV tokens/s of the whole call (wall
 clock around K back-to-back steps, inputs resident in HBM); `roofline` uses
 the fused kernel's own duration, measured with HIP events on its launch
-stream; `cpu_baseline` times the CPU oracle (a single-threaded numpy/torch
-restatement) on a time-bounded sample of the same workload.
+stream; `cpu_baseline` times the CPU oracle's C restatement (OpenMP, up to 16
+host threads) on a time-bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -454,17 +454,37 @@ def run_config5(steps, warmup, seed=0):
     return out
 
 
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the cores this process may run on,
+    at most 16 (one GPU's share of the box)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
 def run_cpu_baseline(cfg, budget_s=12.0):
     """The CPU oracle's fused scatter + re-rotate over the whole workload (all
     layers, 256 jobs) with a reduced 1024-block pool (same bytes moved): one
-    warm-up run, then repeated runs until `budget_s` has elapsed (at most 5);
-    the median run time gives tokens/s."""
+    warm-up run, then repeated runs until `budget_s` has elapsed (at most 20);
+    the median run time gives tokens/s. It runs the oracle's C restatement
+    (oracle/c/oracle_copy.c) on cpu_threads() OpenMP threads, or the numpy
+    oracle on one thread when the C library has not been built."""
+    from oracle import native
     from oracle.copy import OracleCopier
-    torch.set_num_threads(1)
+    threads = cpu_threads()
+    if native.available():
+        oc = native.NativeOracleCopier(threads)
+        what = f"the C restatement oracle/c/oracle_copy.c on {threads} OpenMP threads"
+    else:
+        torch.set_num_threads(1)
+        threads = 1
+        oc = OracleCopier()
+        what = "the numpy oracle oracle/copy.py on one thread"
     w = build_workload(cfg, torch.device("cpu"), num_blocks=1024)
     j = w["jobs"]
     inv = w["inv_freq"].numpy()
-    oc = OracleCopier()
     for name, t in zip(w["names"], w["cache"]):
         oc.register_layer(name, t, False)
     oc.register_store(w["staging"])
@@ -476,16 +496,16 @@ def run_cpu_baseline(cfg, budget_s=12.0):
 
     run()
     times = []
-    while len(times) < 5 and sum(times) < budget_s:
+    while len(times) < 20 and sum(times) < budget_s:
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     T = w["T"]
-    return dict(value=T / med, unit="reused KV tokens/s", cores=1, kind="port",
+    return dict(value=T / med, unit="reused KV tokens/s", cores=threads, kind="port",
                 sample=f"whole workload (32 layers x 8 chunks x 1024 tokens, 1024-block pool) through "
-                       f"the CPU oracle oracle/copy.py scatter_pages_rerotate, one thread, median of "
-                       f"{len(times)} runs ({med:.2f} s each) after one warm-up",
+                       f"scatter_pages_rerotate of {what}, median of {len(times)} runs "
+                       f"({med:.3f} s each) after one warm-up",
                 GBps=algorithmic_bytes(cfg) / med / 1e9)
 
 

@@ -196,7 +196,10 @@ typedef struct daric_rope_segment {
  * does not change the result: the rotation is linear, so the stored codes are
  * rotated directly (rot(q * s) / s = rot(q)), as the reference's kernel
  * rotates the raw fp8 values (adapter.py:30-88). `block_table` is a 1-D
- * contiguous int32 device tensor. */
+ * contiguous int32 device tensor. Every slot must be listed at most once
+ * across the segments: workgroups rotate their tokens concurrently, so a
+ * repeated slot gets an unspecified result (one program per token races the
+ * same way in the reference). */
 int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers, int page_first,
                          const daric_tensor* block_table,
                          const daric_rope_segment* segments, int64_t n_segments,

@@ -14,6 +14,11 @@ function on the path, each citing the reference file:line it follows:
              kernels; the reference has no such kernel)
   kvio.py    store/load record format and copy plan of the daric-store GPU I/O
              (daric/management/service/gpu_kv_io.py)
+  c/oracle_copy.c + native.py
+             a second, independent restatement in C (OpenMP) of the page
+             copies and the fused scatter + re-rotation, built by build.py;
+             byte-identical to copy.py on every layout and dtype
+             (tests/test_oracle_native.py) and timed as bench.py's CPU baseline
 
 The recompute budget (daric/adaption/policy.py) is host logic of the product
 (daric_amd/policy.py) and is pinned by vectors of the reference's own function
