@@ -311,7 +311,6 @@ ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_j
         j.layer = static_cast<uint8_t*>(t.data);
         j.stage = store + offsets[i];
         j.idx = idx + indices_offsets[i];
-        j.k_scale = r.layers[i]->k_scale;
         j.prefix_stride = s.prefix_stride;
         j.page_stride = s.page_stride;
         j.span = s.suffix;
@@ -567,7 +566,6 @@ int daric_copier_scatter_pages_rerotate(daric_copier* c, const char* const* name
             gd.ipr = FastDiv(gd.g.ipr);
             gd.tok_div = FastDiv(gd.g.tok_div);
             gd.ps = FastDiv(gd.g.PS);
-            gd.h = FastDiv(gd.g.H);
             DescUpload up(r.device, gr.jobs.data(), gr.jobs.size() * sizeof(CopyJob), st);
             launch_scatter_rotate(static_cast<const CopyJob*>(up.get()), static_cast<int>(gr.jobs.size()),
                                   static_cast<int>(gr.max_tiles), gd, gr.kind, rope->is_neox != 0,

@@ -134,7 +134,8 @@ __global__ __launch_bounds__(kThreads) void copy_pages_kernel(const CopyJob* __r
 // that are not rotated (V rows, tokens past the job's n_tokens) are copied
 // bit-exactly. The first round's loads are issued before the workgroup
 // computes the tile's cos/sin values into LDS, so the sincos latency overlaps
-// the memory latency.
+// the memory latency. fp8 codes are rotated as stored: a per-head scale
+// cancels in a linear rotation.
 template <int KIND, bool NEOX>
 __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
     const CopyJob* __restrict__ jobs, FastDiv njobs, RowGeomDiv gd,
@@ -165,11 +166,10 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
     const int partner = NEOX ? half / VE : 0;      // unit distance of pair halves
     const int pass0 = NEOX ? 2 * g.n_rot : g.n_rot;  // first pass-through unit
     const int items = g.n_rows * g.ipr;
-    const float* __restrict__ ksc = j.k_scale;
 
     for (int base = 0; base < items; base += kThreads * kRotUnroll) {
         u32x4 a[kRotUnroll], b[kRotUnroll];
-        int ua[kRotUnroll], kk[kRotUnroll], rr[kRotUnroll];
+        int ua[kRotUnroll], kk[kRotUnroll];
         bool rot[kRotUnroll], pair[kRotUnroll], ok[kRotUnroll];
 #pragma unroll
         for (int u = 0; u < kRotUnroll; ++u) {
@@ -178,7 +178,6 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
             const int r = static_cast<int>(gd.ipr.div(static_cast<uint32_t>(it)));
             const int k = it - r * g.ipr;
             const int row0 = r * upr;
-            rr[u] = r;
             kk[u] = k;
             if (k < g.n_rot) {
                 ua[u] = row0 + k;
@@ -213,20 +212,11 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
                 if (pair[u]) st_nt(dst + ua[u] + partner, b[u]);
                 continue;
             }
-            float scale = 1.0f;
-            if (KIND == kE4M3 && ksc != nullptr) {
-                const uint32_t r = static_cast<uint32_t>(rr[u]);
-                const int h = g.tok_div == 1
-                    ? static_cast<int>(gd.ps.div(r) - gd.h.div(gd.ps.div(r)) * g.H)
-                    : static_cast<int>(r - gd.h.div(r) * g.H);
-                scale = ksc[h];
-            }
-            const float inv = 1.0f / scale;
             float x[VE];
-            E::unpack(a[u], x, scale);
+            E::unpack(a[u], x, 1.0f);
             if (NEOX) {
                 float y[VE];
-                E::unpack(b[u], y, scale);
+                E::unpack(b[u], y, 1.0f);
                 const int i0 = kk[u] * VE;
 #pragma unroll
                 for (int e = 0; e < VE; ++e) {
@@ -235,8 +225,8 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
                     x[e] = x1 * c - x2 * sn;
                     y[e] = x2 * c + x1 * sn;
                 }
-                st_nt(dst + ua[u], E::pack(x, inv));
-                st_nt(dst + ua[u] + partner, E::pack(y, inv));
+                st_nt(dst + ua[u], E::pack(x, 1.0f));
+                st_nt(dst + ua[u] + partner, E::pack(y, 1.0f));
             } else {
                 const int i0 = kk[u] * (VE / 2);
 #pragma unroll
@@ -246,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
                     x[2 * m] = x1 * c - x2 * sn;
                     x[2 * m + 1] = x2 * c + x1 * sn;
                 }
-                st_nt(dst + ua[u], E::pack(x, inv));
+                st_nt(dst + ua[u], E::pack(x, 1.0f));
             }
         }
     }

@@ -15,7 +15,6 @@ struct alignas(16) CopyJob {
     uint8_t* layer;
     uint8_t* stage;
     const int32_t* idx;
-    const float* k_scale;     // fp8 layers: H per-head scales (nullptr = 1)
     int64_t prefix_stride;
     int64_t page_stride;
     int64_t span;

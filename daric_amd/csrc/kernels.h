@@ -31,7 +31,7 @@ struct FastDiv {
 
 struct RowGeomDiv {
     RowGeom g;
-    FastDiv ipr, tok_div, ps, h;
+    FastDiv ipr, tok_div, ps;
 };
 
 // Plain page copies. vw is the access width in bytes (16, 4 or 1); max_span

@@ -106,9 +106,13 @@ def test_fused_pairing_partial_rotary(dev, neox, rotary_dim):
     fused_case(dev, "nhd", torch.bfloat16, neox, rotary_dim, seed=2)
 
 
-@pytest.mark.parametrize("layout", ["nhd", "pf", "packed"])
-def test_fused_fp8(dev, layout):
-    fused_case(dev, layout, torch.uint8, True, 64, d=128 if layout != "packed" else 64, seed=3)
+@pytest.mark.parametrize("layout", ["nhd", "pf", "packed", "mla"])
+@pytest.mark.parametrize("neox", [True, False])
+def test_fused_fp8(dev, layout, neox):
+    # mla: 576-byte rows (36 units, not a divisor of the wavefront) take the
+    # item-based kernel; the other layouts take the lane-exchange kernel
+    d = {"packed": 64, "mla": 144}.get(layout, 128)
+    fused_case(dev, layout, torch.uint8, neox, 64, d=d, seed=3)
 
 
 def test_fused_llama3_8b_page_shape(dev):
@@ -175,6 +179,12 @@ def test_inplace_layouts(dev, layout, dtype):
 def test_inplace_pairing_and_element_path(dev, neox, rotary_dim):
     # rotary_dim 24 / 10 take the per-element kernel (pairs not 16-byte aligned)
     inplace_case(dev, "nhd", torch.bfloat16, neox, rotary_dim, seed=5)
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_inplace_fp8_element_path(dev, neox):
+    # rotary_dim 24 on fp8: pair halves of 12 bytes take the per-element kernel
+    inplace_case(dev, "nhd", torch.uint8, neox, 24, d=128, seed=6)
 
 
 def test_fp8_identity_rotation_is_exact(dev):
