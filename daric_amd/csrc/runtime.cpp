@@ -31,6 +31,9 @@ std::string fmt_dims(const int64_t* v, int n) {
 }
 
 bool is_contiguous(const daric_tensor& t) {
+    // as torch: a tensor without elements is contiguous whatever its strides
+    for (int d = 0; d < t.ndim; ++d)
+        if (t.sizes[d] == 0) return true;
     int64_t expected = 1;
     for (int d = t.ndim - 1; d >= 0; --d) {
         if (t.sizes[d] == 1) continue;

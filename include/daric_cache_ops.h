@@ -223,11 +223,13 @@ typedef struct daric_chunk {
 } daric_chunk;
 
 /* keys[l, row_offset + j] = sum over (h, d) of (k_new[l, row, h, d] - K_cache)^2
- * in fp32, in the fixed order documented in daric_amd/csrc/select.hip.
+ * in fp32, in the fixed order documented in daric_amd/csrc/select_kernels.hip.
  * layers: n_layers paged caches (same geometry); k_new: [n_layers, T, H, D]
  * contiguous, bf16 or fp16; keys: [n_layers, T] fp32 contiguous. For an fp8
  * (e4m3) cache, k_scales is NULL (scale 1) or an [n_layers, H] fp32 device
- * tensor: cached K is dequantised as float32(code value * scale[l, h]). */
+ * tensor: cached K is dequantised as float32(code value * scale[l, h]). A
+ * token whose block id lies outside [0, num_blocks) is not read and gets
+ * key 0. Rows of keys outside every chunk are not written. */
 int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_first,
                        const daric_tensor* block_table, const daric_tensor* k_new,
                        const daric_chunk* chunks, int64_t n_chunks,

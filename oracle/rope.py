@@ -123,11 +123,16 @@ def rerotate_pages(layers, page_first: bool, block_table, segments, inv_freq,
                    rotary_dim: int, is_neox: bool, k_scales=None) -> None:
     """In-place re-rotation of every segment (bt_offset, tok_start, n_tokens,
     delta) in every layer: the counterpart of one _launch_triton_rerotate per
-    layer over the concatenated gather_idx of the segments."""
+    layer over the concatenated gather_idx of the segments. A segment with
+    delta 0 is left alone, as apply_rerotate_load leaves a chunk whose saved
+    and new positions agree (adapter.py:212); rotating it by the identity
+    would still turn some -0 values into +0."""
     for li, layer in enumerate(layers):
         ps = k_view(layer, page_first, rotary_dim).shape[1]
         ks = None if k_scales is None else np.asarray(k_scales[li])
         for bt_offset, tok_start, n_tokens, delta in segments:
+            if int(delta) == 0:
+                continue
             slots = segment_slots(block_table, bt_offset, tok_start, n_tokens, ps)
             rotate_slots(layer, page_first, slots, delta, inv_freq, rotary_dim, is_neox, ks)
 

@@ -98,18 +98,23 @@ def chunk_slots(block_table, bt_offset, n_tokens, page_size):
 
 def deviation(layers, page_first, block_table, k_new, chunks, k_scales=None) -> np.ndarray:
     """keys [L, T] for chunks (bt_offset, row_offset, n_tokens, k); rows of T
-    not covered by any chunk are left 0."""
+    not covered by any chunk are left 0, and so are tokens whose block id lies
+    outside [0, num_blocks)."""
     L, T = len(layers), k_new.shape[1]
     keys = np.zeros((L, T), np.float32)
     for l, layer in enumerate(layers):
         kv = k_rows_view(layer, page_first)
         ps, h, d = kv.shape[1], kv.shape[2], kv.shape[3]
         ks = None if k_scales is None else k_scales[l]
+        nb = kv.shape[0]
         for bt_offset, row_offset, n_tokens, _k in chunks:
             blk, s = chunk_slots(block_table, bt_offset, n_tokens, ps)
-            cached = _as_f32(kv[torch.as_tensor(blk), torch.as_tensor(s)], ks).reshape(n_tokens, h * d)
+            ok = (blk >= 0) & (blk < nb)        # other block ids: not read, key 0
+            cached = _as_f32(kv[torch.as_tensor(np.where(ok, blk, 0)), torch.as_tensor(s)], ks)
+            cached = cached.reshape(n_tokens, h * d)
             new = k_new[l, row_offset: row_offset + n_tokens].to(torch.float32).numpy().reshape(n_tokens, h * d)
-            keys[l, row_offset: row_offset + n_tokens] = fixed_order_sumsq(new, cached)
+            key = fixed_order_sumsq(new, cached)
+            keys[l, row_offset: row_offset + n_tokens] = np.where(ok, key, np.float32(0.0))
     return keys
 
 

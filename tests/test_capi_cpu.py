@@ -183,6 +183,8 @@ def test_register_errors(lib):
     assert c.register_store(fake((16,), torch.int32)) == "store buffer must be uint8"
     assert c.register_store(fake((16,), torch.uint8, device=-1)) == "staging buffer must be on CUDA"
     assert c.register_store(fake((16,), torch.uint8, strides=(2,))) == "store buffer must be contiguous"
+    # as torch: a tensor without elements is contiguous whatever its strides
+    assert c.register_store(fake((0,), torch.uint8, strides=(2,))) is None
 
 
 def test_rerotate_layout_errors(lib):

@@ -123,6 +123,22 @@ def test_rerotate_pages_in_place(page_first):
     assert torch.equal(v_a.view(torch.int16), v_b.view(torch.int16))
 
 
+def test_zero_shift_segment_is_untouched():
+    # delta 0 leaves every byte alone, -0 codes included (an identity rotation
+    # computes -0*1 - (-0)*0 = +0)
+    layer = torch.zeros(2, 4, 4, 2, 16, dtype=torch.uint8)
+    layer[0] = 0x80                                   # fp8 -0 everywhere in K
+    before = layer.clone()
+    inv = rope.default_inv_freq(16, 10000.0)
+    rope.rerotate_pages([layer], False, np.array([1, 2], np.int32), [(0, 0, 8, 0)], inv, 16, True,
+                        np.ones((1, 2)))
+    assert torch.equal(layer, before)
+    # the same rows rotated by a non-zero shift do change sign of zero somewhere
+    rope.rerotate_pages([layer], False, np.array([1, 2], np.int32), [(0, 0, 8, 5)], inv, 16, True,
+                        np.ones((1, 2)))
+    assert not torch.equal(layer, before)
+
+
 def test_segment_planning():
     # apply_rerotate_load: metas with saved_pos == ptr[0] or empty are skipped
     bt, segs = rope.load_segments([(0, 32, 0, [4, 5]), (32, 64, 0, [6, 7]),

@@ -94,6 +94,24 @@ def test_deviation_uses_slots():
         assert abs(keys[0, j] - ref) <= 1e-5 * ref
 
 
+def test_deviation_out_of_range_block_gives_zero_key():
+    # block ids outside [0, num_blocks) are not read and give key 0 (negative
+    # ids must not wrap around as Python indexing would); block 0 is read
+    g = torch.Generator().manual_seed(3)
+    nb, ps, h, d = 5, 4, 2, 8
+    layer = torch.randn(2, nb, ps, h, d, generator=g).to(torch.bfloat16)
+    bt = np.array([-1, 0, nb, 3], np.int32)
+    k_new = torch.randn(1, 16, h, d, generator=g).to(torch.bfloat16)
+    keys = select.deviation([layer], False, bt, k_new, [(0, 0, 16, 2)])
+    for j in range(16):
+        blk = int(bt[j // ps])
+        if blk < 0 or blk >= nb:
+            assert keys[0, j] == 0.0
+        else:
+            ref = ((k_new[0, j].double() - layer[0, blk, j % ps].double()) ** 2).sum().item()
+            assert abs(keys[0, j] - ref) <= 1e-5 * ref
+
+
 def test_deviation_fp8_dequantises_with_per_head_scale():
     """fp8 cache: cached K is code value x scale[layer, head] (float64 check,
     independent of the fixed order); no scales means scale 1."""
