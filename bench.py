@@ -273,6 +273,52 @@ def run_config3(steps, warmup, seed=0):
     return out
 
 
+def run_config2_hnd(steps, warmup, seed=0):
+    """Config 2's return path on a head-major cache: the request's 8 x 1024
+    tokens in 32 layers of a [2, 65536, 16, 8, 128] bf16 cache stored HND
+    ([2, NB, H, PS, D] in memory), gathered token-major into [L, 2, T, H, D]
+    (gather_tokens: the LDS-transpose kernel) and scattered back
+    (scatter_tokens). gather_pages of the same pages -- the reference's
+    physical-span staging, no transpose -- is timed beside them. The cache is
+    left uninitialised: the kernels copy bytes, whatever their values."""
+    from daric_amd import cache_ops
+    c = CFG2
+    dev = torch.device("cuda:0")
+    L, H, D, PS, NB = c["layers"], c["kv_heads"], c["head_dim"], c["block_size"], c["num_blocks"]
+    T = c["chunks"] * c["chunk_tokens"]
+    n_pages = T // PS
+    g = torch.Generator().manual_seed(seed)
+    ids = (torch.randperm(NB - 1, generator=g)[:n_pages] + 1).to(torch.int32)
+    names = layer_names(L)
+    cache = [torch.empty(2, NB, H, PS, D, device=dev, dtype=torch.bfloat16).permute(0, 1, 3, 2, 4)
+             for _ in range(L)]
+    per_layer = 2 * T * H * D * 2
+    staging = torch.empty(L * per_layer, dtype=torch.uint8, device=dev)
+    cp = cache_ops.CacheCopier()
+    for n, t in zip(names, cache):
+        cp.register_layer(n, t, False)
+    cp.register_store(staging)
+    flat = torch.cat([ids] * L).to(dev)
+    offs = [i * per_layer for i in range(L)]
+    sizes = [per_layer] * L
+    ioff = [i * n_pages for i in range(L + 1)]
+    stream = torch.cuda.current_stream(dev)
+    out = {"workload": "config 2 return path on an HND cache ([2, 65536, H=8, PS=16, D=128] bf16 in memory), "
+                       "32 layers x 8192 tokens to token-major [L, 2, T, H, D] and back",
+           "tokens": T}
+    nbytes = 2 * L * per_layer
+    for key, fn in (("gather_tokens", cp.gather_tokens), ("scatter_tokens", cp.scatter_tokens),
+                    ("gather_pages_physical_span", cp.gather_pages)):
+        r = time_steps(lambda fn=fn: fn(names, offs, sizes, flat, ioff, stream.cuda_stream),
+                       steps, warmup, stream)
+        out[key] = {"ms": r["step_ms"], "kernel_ms": r["kern_ms"], "GBps": _gbps(nbytes, r["kern_ms"]),
+                    "frac": _gbps(nbytes, r["kern_ms"]) / PEAK_HBM_GBPS}
+    out["algorithmic_bytes"] = nbytes
+    del cache, staging
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_config4(steps, warmup, seed=0):
     """KV offload/load: 65536 tokens (4096 pages) of a
     Llama-3-8B bf16 cache with a seeded random block table. Store: gather the
@@ -544,7 +590,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--extra", default="3,4,5",
+    ap.add_argument("--extra", default="2h,3,4,5",
                     help="other BASELINE configs to measure after the headline (comma list, or 'none')")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (torch copy_) `steps` times, the "
@@ -565,7 +611,7 @@ def main():
     g_achieved = nbytes / (r["g_kern_ms"] / 1e3) / 1e9
     torch.cuda.empty_cache()
     extra = {}
-    runners = {"3": run_config3, "4": run_config4, "5": run_config5}
+    runners = {"2h": run_config2_hnd, "3": run_config3, "4": run_config4, "5": run_config5}
     for cname in [x.strip() for x in a.extra.split(",") if x.strip() and x.strip() != "none"]:
         extra[f"config{cname}"] = runners[cname](max(3, a.steps // 2), max(1, a.warmup))
     cpu = None if a.no_cpu else run_cpu_baseline(cfg, a.cpu_budget)

@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libdaric_cache_ops.so")
 MAX_DIMS = 8
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_CODES = {
     torch.uint8: 0,
@@ -74,6 +74,10 @@ SIGNATURES = {
                                           c_int64, c_uint64]),
     "daric_copier_scatter_pages": (c_int, [c_void_p, STRS, c_int64, I64P, c_int64, I64P, c_int64, T, I64P,
                                            c_int64, c_uint64]),
+    "daric_copier_gather_tokens": (c_int, [c_void_p, STRS, c_int64, I64P, c_int64, I64P, c_int64, T, I64P,
+                                           c_int64, c_uint64]),
+    "daric_copier_scatter_tokens": (c_int, [c_void_p, STRS, c_int64, I64P, c_int64, I64P, c_int64, T, I64P,
+                                            c_int64, c_uint64]),
     "daric_copier_scatter_pages_rerotate": (c_int, [c_void_p, STRS, c_int64, I64P, c_int64, I64P, c_int64, T,
                                                     I64P, c_int64, I64P, I64P, P(DaricRope), c_uint64]),
     "daric_batched_memcpy_d2h": (c_int, [T, T, I64P, I64P, I64P, c_int64, c_uint64]),

@@ -22,7 +22,8 @@ BUILD = os.path.join(ROOT, "_build")
 LIB = os.path.join(LIBDIR, "libdaric_cache_ops.so")
 HOSTTEST_LIB = os.path.join(LIBDIR, "libdaric_hosttest.so")
 
-SOURCES = ["capi.cpp", "runtime.cpp", "copy_kernels.hip", "rope_kernels.hip", "select_kernels.hip"]
+SOURCES = ["capi.cpp", "runtime.cpp", "copy_kernels.hip", "rope_kernels.hip", "select_kernels.hip",
+           "token_kernels.hip"]
 
 ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",

@@ -8,7 +8,9 @@ argument meaning and errors (RuntimeError with the reference's message text).
 
 Additions (no reference counterpart; the .pyi grows, nothing changes):
   CacheCopier.register_k_scale, CacheCopier.scatter_pages_rerotate,
-  rerotate_pages, kv_deviation, topk_per_chunk, merge_rows, kernel timing.
+  CacheCopier.gather_tokens / scatter_tokens (token-major staging for any
+  cache layout), rerotate_pages, kv_deviation, topk_per_chunk, merge_rows,
+  kernel timing.
 
 Every call is asynchronous on `stream` (0 = the current torch stream of the
 first layer's device, as in reference copier.cpp:27-30). The wrapper keeps
@@ -151,6 +153,23 @@ class CacheCopier:
                       byte_sizes: Sequence[int], indices_flat: torch.Tensor,
                       indices_offsets: Sequence[int], stream: int = 0) -> None:
         self._copy(self._lib.daric_copier_scatter_pages, layer_names, offsets, byte_sizes,
+                   indices_flat, indices_offsets, stream)
+
+    def gather_tokens(self, layer_names: Sequence[str], offsets: Sequence[int],
+                      byte_sizes: Sequence[int], indices_flat: torch.Tensor,
+                      indices_offsets: Sequence[int], stream: int = 0) -> None:
+        """gather_pages into token-major rows: job i's store range becomes
+        [n_kv][n_sel * PS][H][D] (K rows then V rows) for any cache layout
+        (see include/daric_cache_ops.h). byte_sizes[i] = n_kv * n_sel * PS *
+        H * D * element size. No counterpart in the reference."""
+        self._copy(self._lib.daric_copier_gather_tokens, layer_names, offsets, byte_sizes,
+                   indices_flat, indices_offsets, stream)
+
+    def scatter_tokens(self, layer_names: Sequence[str], offsets: Sequence[int],
+                       byte_sizes: Sequence[int], indices_flat: torch.Tensor,
+                       indices_offsets: Sequence[int], stream: int = 0) -> None:
+        """Inverse of gather_tokens. No counterpart in the reference."""
+        self._copy(self._lib.daric_copier_scatter_tokens, layer_names, offsets, byte_sizes,
                    indices_flat, indices_offsets, stream)
 
     def scatter_pages_rerotate(self, layer_names: Sequence[str], offsets: Sequence[int],

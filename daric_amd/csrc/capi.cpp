@@ -252,16 +252,17 @@ struct ResolvedJobs {
     int device = -1;
 };
 
-// Shared front half of gather/scatter: the reference's check order
-// (copier.cpp:46-66) followed by the launcher's per-job shape and byte-size
-// checks (kernels.cu:135-161).
-ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_jobs,
-                          const int64_t* offsets, int64_t n_offsets, const int64_t* byte_sizes,
-                          int64_t n_byte_sizes, const daric_tensor* indices,
-                          const int64_t* indices_offsets, int64_t n_indices_offsets, bool gather) {
-    ResolvedJobs r;
+// Shared front half of every page-list copy: the reference's check order
+// (copier.cpp:46-66). Returns the jobs' layers (empty for an empty job list).
+std::vector<daric_copier::Layer*> resolve_front(daric_copier* c, const char* const* names,
+                                               int64_t n_jobs, const int64_t* offsets,
+                                               int64_t n_offsets, const int64_t* byte_sizes,
+                                               int64_t n_byte_sizes, const daric_tensor* indices,
+                                               const int64_t* indices_offsets,
+                                               int64_t n_indices_offsets, bool gather) {
+    std::vector<daric_copier::Layer*> layers;
     DARIC_CHECK(c->has_store, "store buffer not registered; call register_store() first");
-    if (n_jobs == 0) return r;
+    if (n_jobs == 0) return layers;
     DARIC_CHECK(n_jobs > 0 && names != nullptr, "layer_names must not be empty");
     DARIC_CHECK(n_jobs <= kIntMax, "too many jobs in one call: ", n_jobs);
     validate_common_job_inputs(n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices_offsets,
@@ -273,22 +274,36 @@ ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_j
         DARIC_CHECK(offsets[i] <= store_size, "store offset out of range at job ", i);
         DARIC_CHECK(byte_sizes[i] <= store_size - offsets[i], "store range out of bounds at job ", i);
     }
-    r.layers.reserve(n_jobs);
+    layers.reserve(n_jobs);
     for (int64_t i = 0; i < n_jobs; ++i) {
         DARIC_CHECK(names[i] != nullptr, "layer not registered: (null)");
         auto it = c->by_name.find(std::string_view(names[i]));
         DARIC_CHECK(it != c->by_name.end(), "layer not registered: ", names[i]);
-        r.layers.push_back(it->second);
+        layers.push_back(it->second);
     }
-    r.device = r.layers[0]->t.device;
-    DARIC_CHECK(indices->device == r.device, "indices_flat must be on the same device as kvcache");
+    const int device = layers[0]->t.device;
+    DARIC_CHECK(indices->device == device, "indices_flat must be on the same device as kvcache");
     for (int64_t i = 0; i < n_jobs; ++i) {
-        DARIC_CHECK(r.layers[i]->t.device >= 0, gather ? "all source layers must be CUDA tensors; job "
-                                                       : "all destination layers must be CUDA tensors; job ", i);
-        DARIC_CHECK(r.layers[i]->t.device == r.device,
+        DARIC_CHECK(layers[i]->t.device >= 0, gather ? "all source layers must be CUDA tensors; job "
+                                                     : "all destination layers must be CUDA tensors; job ", i);
+        DARIC_CHECK(layers[i]->t.device == device,
                     gather ? "all source layers must be on the same device; job "
                            : "all destination layers must be on the same device; job ", i);
     }
+    return layers;
+}
+
+// gather/scatter_pages: the front half, then the launcher's per-job shape and
+// byte-size checks (kernels.cu:135-161).
+ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_jobs,
+                          const int64_t* offsets, int64_t n_offsets, const int64_t* byte_sizes,
+                          int64_t n_byte_sizes, const daric_tensor* indices,
+                          const int64_t* indices_offsets, int64_t n_indices_offsets, bool gather) {
+    ResolvedJobs r;
+    r.layers = resolve_front(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices,
+                             indices_offsets, n_indices_offsets, gather);
+    if (r.layers.empty()) return r;
+    r.device = r.layers[0]->t.device;
     uint8_t* store = static_cast<uint8_t*>(c->store.data);
     const int32_t* idx = static_cast<const int32_t*>(indices->data);
     r.jobs.resize(n_jobs);
@@ -332,6 +347,127 @@ ResolvedJobs resolve_jobs(daric_copier* c, const char* const* names, int64_t n_j
     DARIC_CHECK(r.max_tiles <= kMaxTiles, "too many pages in one job: ", r.max_tiles);
     r.vw = a16 ? 16 : (a4 ? 4 : 1);
     return r;
+}
+
+// Token-major view of a KV layer for gather/scatter_tokens, in elements.
+struct TokenLayout {
+    int64_t PS, H, D, sb, ss, sh, v_off, num_blocks;
+    int n_kv;
+};
+
+TokenLayout token_layout(const daric_tensor& t, bool page_first) {
+    TokenLayout r{};
+    if (t.ndim == 5) {
+        // [2, NB, PS, H, D] or page-first [NB, 2, PS, H, D], any strides
+        r.PS = t.sizes[2]; r.H = t.sizes[3]; r.D = t.sizes[4];
+        const int kv_dim = page_first ? 1 : 0;
+        DARIC_CHECK(t.sizes[kv_dim] == 2, "token-major copies need a K/V dimension of size 2, got shape=",
+                    sizes_str(t));
+        r.v_off = t.strides[kv_dim];
+        r.sb = t.strides[page_first ? 0 : 1];
+        r.num_blocks = t.sizes[page_first ? 0 : 1];
+        r.ss = t.strides[2]; r.sh = t.strides[3];
+        r.n_kv = 2;
+        DARIC_CHECK(t.strides[4] == 1 || r.D == 1, "KV cache head_dim stride must equal 1 for token-major copies");
+    } else if (t.ndim == 4) {
+        // packed [NB, H, PS, 2D]: K in [0, D), V in [D, 2D) of every row
+        DARIC_CHECK(page_first, "a 4-D (packed) KV cache must be page_first");
+        DARIC_CHECK(t.sizes[3] > 0 && t.sizes[3] % 2 == 0 && t.strides[3] == 1,
+                    "packed KV rows must have an even, contiguous last dimension, got shape=", sizes_str(t),
+                    ", stride=", strides_str(t));
+        r.PS = t.sizes[2]; r.H = t.sizes[1]; r.D = t.sizes[3] / 2;
+        r.sb = t.strides[0]; r.ss = t.strides[2]; r.sh = t.strides[1];
+        r.v_off = r.D;
+        r.num_blocks = t.sizes[0];
+        r.n_kv = 2;
+    } else if (t.ndim == 3) {
+        // MLA [NB, PS, hidden]: one latent row per token, no V
+        r.PS = t.sizes[1]; r.H = 1; r.D = t.sizes[2];
+        r.sb = t.strides[0]; r.ss = t.strides[1]; r.sh = 0; r.v_off = 0;
+        r.num_blocks = t.sizes[0];
+        r.n_kv = 1;
+        DARIC_CHECK(t.strides[2] == 1 || r.D == 1, "KV cache hidden stride must equal 1 for token-major copies");
+    } else {
+        throw Error(DARIC_ERR_INVALID, cat("Unsupported KV cache rank for token-major copies: ", t.ndim));
+    }
+    DARIC_CHECK(r.PS > 0 && r.H > 0 && r.D > 0, "token-major copies need non-empty pages, got shape=",
+                sizes_str(t));
+    DARIC_CHECK(r.num_blocks <= kIntMax && r.PS <= kIntMax && r.H <= kIntMax && r.D * t.elem_size <= kIntMax,
+                "KV cache dimensions exceed int range");
+    return r;
+}
+
+int copy_tokens(daric_copier* c, const char* const* names, int64_t n_jobs, const int64_t* offsets,
+                int64_t n_offsets, const int64_t* byte_sizes, int64_t n_byte_sizes,
+                const daric_tensor* indices, const int64_t* indices_offsets,
+                int64_t n_indices_offsets, uint64_t stream, bool gather) {
+    return guarded([&] {
+        DARIC_CHECK(c != nullptr, "copier must not be null");
+        std::lock_guard<std::mutex> lk(c->mu);
+        const auto layers = resolve_front(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes,
+                                          indices, indices_offsets, n_indices_offsets, gather);
+        if (layers.empty()) return;
+        const int device = layers[0]->t.device;
+        uint8_t* store = static_cast<uint8_t*>(c->store.data);
+        const int32_t* idx = static_cast<const int32_t*>(indices->data);
+        std::vector<TokenJob> jobs(n_jobs);
+        std::vector<int64_t> units_per_row(n_jobs);
+        bool vec = true, lds = true;
+        for (int64_t i = 0; i < n_jobs; ++i) {
+            const daric_tensor& t = layers[i]->t;
+            if (layers[i]->shape_status != DARIC_OK) throw Error(layers[i]->shape_status, layers[i]->shape_msg);
+            const TokenLayout L = token_layout(t, layers[i]->page_first);
+            const int64_t e = t.elem_size;
+            const int64_t n_sel = indices_offsets[i + 1] - indices_offsets[i];
+            const int64_t num = L.n_kv * n_sel * L.PS * L.H * L.D * e;
+            if (byte_sizes[i] != num)
+                throw Error(DARIC_ERR_RUNTIME,
+                            cat("byte_size mismatch at job ", i, " | C++ expected bytes: ", num,
+                                " | Python passed bytes: ", byte_sizes[i], " | Tensor shape: ",
+                                sizes_str(t), " | Tensor strides: ", strides_str(t)));
+            DARIC_CHECK(n_sel <= kIntMax, "too many selected pages at job ", i);
+            TokenJob& j = jobs[i];
+            j.layer = static_cast<uint8_t*>(t.data);
+            j.stage = store + offsets[i];
+            j.idx = idx + indices_offsets[i];
+            j.sb = L.sb * e; j.ss = L.ss * e; j.sh = L.sh * e; j.v_off = L.v_off * e;
+            j.n_sel = static_cast<int32_t>(n_sel);
+            j.num_blocks = static_cast<int32_t>(L.num_blocks);
+            j.PS = static_cast<int32_t>(L.PS);
+            j.H = static_cast<int32_t>(L.H);
+            j.row_bytes = static_cast<int32_t>(L.D * e);
+            j.n_kv = L.n_kv;
+            const bool a16 = j.row_bytes % 16 == 0 && j.sb % 16 == 0 && j.ss % 16 == 0 && j.sh % 16 == 0 &&
+                             j.v_off % 16 == 0 && aligned(t.data, 16) && aligned(j.stage, 16);
+            vec = vec && a16;
+            // head-major dense pages with rows of >= 128 bytes take the LDS transpose
+            lds = lds && a16 && j.H > 1 && j.ss == j.row_bytes && j.sh == static_cast<int64_t>(j.PS) * j.row_bytes &&
+                  j.row_bytes >= 128 && static_cast<int64_t>(j.H) * (j.row_bytes / 16) <= 512;
+        }
+        const int vw = vec ? 16 : 1;
+        int64_t max_parts = 0;
+        for (TokenJob& j : jobs) {
+            const int64_t row_units = j.row_bytes / vw;
+            const int64_t head_units = static_cast<int64_t>(j.H) * row_units;
+            int64_t pt;
+            if (lds) pt = std::max<int64_t>(1, 512 / head_units);                 // 8 KiB of LDS
+            else pt = std::max<int64_t>(1, (vw == 16 ? 16384 : 4096) / (static_cast<int64_t>(j.H) * j.row_bytes));
+            pt = std::min<int64_t>(pt, j.PS);
+            j.part_tokens = static_cast<int32_t>(pt);
+            j.parts_per_page = static_cast<int32_t>((j.PS + pt - 1) / pt);
+            j.d_upr = FastDiv(static_cast<uint32_t>(row_units));
+            j.d_h = FastDiv(static_cast<uint32_t>(j.H));
+            DARIC_CHECK(pt * head_units <= kIntMax, "page part exceeds int range");
+            max_parts = std::max<int64_t>(max_parts, static_cast<int64_t>(j.n_kv) * j.n_sel * j.parts_per_page);
+        }
+        if (max_parts == 0) return;
+        DARIC_CHECK(max_parts <= kMaxTiles, "too many pages in one job: ", max_parts);
+        DeviceGuard guard(device);
+        const hipStream_t st = as_stream(stream);
+        DescUpload up(device, jobs.data(), jobs.size() * sizeof(TokenJob), st);
+        launch_token_copy(static_cast<const TokenJob*>(up.get()), static_cast<int>(jobs.size()),
+                          static_cast<int>(max_parts), vw, lds, gather, st);
+    });
 }
 
 int copy_pages(daric_copier* c, const char* const* names, int64_t n_jobs, const int64_t* offsets,
@@ -487,6 +623,24 @@ int daric_copier_scatter_pages(daric_copier* c, const char* const* names, int64_
                               uint64_t stream) {
     return copy_pages(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices,
                       indices_offsets, n_indices_offsets, stream, false);
+}
+
+int daric_copier_gather_tokens(daric_copier* c, const char* const* names, int64_t n_jobs,
+                               const int64_t* offsets, int64_t n_offsets, const int64_t* byte_sizes,
+                               int64_t n_byte_sizes, const daric_tensor* indices,
+                               const int64_t* indices_offsets, int64_t n_indices_offsets,
+                               uint64_t stream) {
+    return copy_tokens(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices,
+                       indices_offsets, n_indices_offsets, stream, true);
+}
+
+int daric_copier_scatter_tokens(daric_copier* c, const char* const* names, int64_t n_jobs,
+                                const int64_t* offsets, int64_t n_offsets, const int64_t* byte_sizes,
+                                int64_t n_byte_sizes, const daric_tensor* indices,
+                                const int64_t* indices_offsets, int64_t n_indices_offsets,
+                                uint64_t stream) {
+    return copy_tokens(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices,
+                       indices_offsets, n_indices_offsets, stream, false);
 }
 
 int daric_copier_scatter_pages_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs,

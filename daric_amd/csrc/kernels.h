@@ -34,6 +34,34 @@ struct RowGeomDiv {
     FastDiv ipr, tok_div, ps;
 };
 
+// One token-major copy job: the pages idx[0 .. n_sel) of one layer to or from
+// staging laid out as [n_kv][n_sel * PS][H][row_bytes] (K rows, then V rows).
+// A workgroup moves one part: part_tokens consecutive tokens (all heads) of
+// one page and one of K or V. Byte units.
+struct alignas(16) TokenJob {
+    uint8_t* layer;          // K element [0, ..., 0] of the layer
+    uint8_t* stage;          // first byte of the job's staging range
+    const int32_t* idx;      // page ids; ids outside [1, num_blocks) are skipped
+    int64_t sb, ss, sh;      // page, token and head strides
+    int64_t v_off;           // V plane relative to K (n_kv == 2)
+    int32_t n_sel;
+    int32_t num_blocks;
+    int32_t PS;
+    int32_t H;
+    int32_t row_bytes;       // D * element size
+    int32_t n_kv;            // 2, or 1 for a cache without V (MLA)
+    int32_t part_tokens;
+    int32_t parts_per_page;  // ceil(PS / part_tokens)
+    FastDiv d_upr;           // row_bytes / access width
+    FastDiv d_h;             // H
+};
+static_assert(sizeof(TokenJob) == 112, "TokenJob layout");
+
+// Token-major gather (staging <- cache) or scatter; lds selects the
+// LDS-staged transpose for head-major pages ([H, PS, D] dense); vw is 16 or 1.
+void launch_token_copy(const TokenJob* d_jobs, int n_jobs, int max_parts, int vw, bool lds,
+                       bool gather, hipStream_t stream);
+
 // Plain page copies. vw is the access width in bytes (16, 4 or 1); max_span
 // is the largest page span (bytes) of the jobs.
 void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int64_t max_span, int vw,

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define DARIC_ABI_VERSION 2
+#define DARIC_ABI_VERSION 3
 
 /* Status codes. */
 #define DARIC_OK 0
@@ -113,8 +113,10 @@ int daric_copier_register_layer(daric_copier* copier, const char* name,
 int daric_copier_register_store(daric_copier* copier, const daric_tensor* buffer);
 
 /* Per-layer fp32 K scales for an fp8 (e4m3) layer: `k_scale` is a device
- * array of H floats (one per KV head). Without it an fp8 layer is rotated
- * with scale 1, which is what the reference does (adapter.py:370-373).
+ * array of at least H positive floats (one per KV head), checked when a fused
+ * job uses the layer. They do not change the result: the rotation is linear,
+ * so a per-head scale cancels and the stored codes are rotated directly, as
+ * the reference rotates the raw fp8 values (adapter.py:370-373).
  * No counterpart in the reference (it has no scaled fp8 path). */
 int daric_copier_register_k_scale(daric_copier* copier, const char* name,
                                   const daric_tensor* k_scale);
@@ -149,8 +151,9 @@ int daric_copier_scatter_pages(daric_copier* copier, const char* const* layer_na
  * Job i rotates the K rows of its first num_tokens[i] tokens (token j is slot
  * j % PS of page j / PS of the job) by deltas[i] positions; V rows, rotary
  * tails and tokens >= num_tokens[i] are copied unchanged. For an fp8 layer
- * the K values are dequantised with the registered per-head scale, rotated
- * in fp32 and requantised (saturating round-to-nearest-even).
+ * the e4m3 codes are decoded, rotated in fp32 and re-encoded (saturating
+ * round-to-nearest-even); a per-head scale would cancel, see
+ * daric_copier_register_k_scale.
  * New entry point; no counterpart in the reference (which scatters in the
  * store process and rotates later in the worker process). */
 int daric_copier_scatter_pages_rerotate(daric_copier* copier,
@@ -162,6 +165,32 @@ int daric_copier_scatter_pages_rerotate(daric_copier* copier,
                                         int64_t n_indices_offsets,
                                         const int64_t* deltas, const int64_t* num_tokens,
                                         const daric_rope* rope, uint64_t stream);
+
+/* Token-major gather: like gather_pages, but job i's store range holds the
+ * selected pages' rows token by token, [n_kv][n_sel * PS][H][D] (K rows, then
+ * V rows; n_kv = 1 for a 3-D MLA cache), whatever the cache layout: NHD
+ * [2, NB, PS, H, D], HND (the same with H and PS swapped in memory),
+ * page-first [NB, 2, PS, H, D], packed [NB, H, PS, 2D] or MLA [NB, PS, hidden].
+ * byte_sizes[i] must equal n_kv * n_sel * PS * H * D * element size. Pages
+ * whose id is 0 or outside [1, num_blocks) are skipped and their rows of the
+ * store left untouched. Same argument checks, in the same order, as
+ * gather_pages. No counterpart in the reference, whose staging is the
+ * physical page span (kernels.cu:20-44): token-major for NHD pages only. */
+int daric_copier_gather_tokens(daric_copier* copier, const char* const* layer_names,
+                               int64_t n_jobs, const int64_t* offsets, int64_t n_offsets,
+                               const int64_t* byte_sizes, int64_t n_byte_sizes,
+                               const daric_tensor* indices_flat,
+                               const int64_t* indices_offsets,
+                               int64_t n_indices_offsets, uint64_t stream);
+
+/* Token-major scatter: inverse of daric_copier_gather_tokens; skipped pages
+ * are not written. No counterpart in the reference. */
+int daric_copier_scatter_tokens(daric_copier* copier, const char* const* layer_names,
+                                int64_t n_jobs, const int64_t* offsets, int64_t n_offsets,
+                                const int64_t* byte_sizes, int64_t n_byte_sizes,
+                                const daric_tensor* indices_flat,
+                                const int64_t* indices_offsets,
+                                int64_t n_indices_offsets, uint64_t stream);
 
 /* batched_memcpy_d2h / batched_memcpy_h2d (reference helpers.cu:187-248):
  * one hipMemcpyAsync per region on `stream`. */

@@ -59,7 +59,7 @@ def test_exports_every_declared_symbol(lib):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover the header"
-    assert lib.daric_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.daric_abi_version() == _lib.ABI_VERSION == 3
 
 
 def fake(shape, dtype, device=0, strides=None, ptr=0x10000000):
@@ -98,9 +98,9 @@ class CCopier:
     def register_store(self, d):
         return self.err(self.lib.daric_copier_register_store(self.h, ctypes.byref(d)))
 
-    def gather(self, names, offsets, sizes, idx, idx_off):
+    def gather(self, names, offsets, sizes, idx, idx_off, fn="daric_copier_gather_pages"):
         off, sz, io = _lib.I64(offsets), _lib.I64(sizes), _lib.I64(idx_off)
-        return self.err(self.lib.daric_copier_gather_pages(
+        return self.err(getattr(self.lib, fn)(
             self.h, _lib.str_array(names), len(names), off.ptr, off.n, sz.ptr, sz.n,
             ctypes.byref(idx), io.ptr, io.n, ctypes.c_uint64(0)))
 
@@ -156,6 +156,48 @@ def test_validation_matches_oracle(lib):
     assert e_c == "indices_flat must be on CUDA"
     e_c = c.gather(["a"], [0], [64], fake((1,), torch.int32, device=1), [0, 1])
     assert e_c == "indices_flat must be on the same device as kvcache"
+
+
+@pytest.mark.parametrize("fn", ["daric_copier_gather_tokens", "daric_copier_scatter_tokens"])
+def test_token_copy_validation_matches_oracle(lib, fn):
+    """gather/scatter_tokens: gather_pages' checks in the same order, then the
+    token-major byte size and layout checks, with the oracle's messages."""
+    c = CCopier(lib)
+    o = OracleCopier()
+    shapes = {"a": ((2, 4, 2, 2, 4), False), "p": ((4, 2, 8), True), "m": ((4, 2, 8), False),
+              "q": ((4, 8), False)}
+    for name, (shape, pf) in shapes.items():
+        assert c.register_layer(name, fake(shape, torch.float16), int(pf)) is None
+        o.register_layer(name, torch.zeros(shape, dtype=torch.float16), pf)
+    idx = fake((2,), torch.int32, ptr=0x20000000)
+    oidx = torch.tensor([1, 2], dtype=torch.int32)
+    ofn = o.gather_tokens if "gather" in fn else o.scatter_tokens
+
+    def both(names, offs, sizes, idx_off):
+        return c.gather(names, offs, sizes, idx, idx_off, fn), oracle_error(
+            lambda: ofn(names, offs, sizes, oidx, idx_off))
+
+    e_c, e_o = both(["a"], [0], [64], [0, 1])
+    assert e_c == e_o and "store buffer not registered" in e_c
+    assert c.register_store(fake((4096,), torch.uint8, ptr=0x30000000)) is None
+    o.register_store(torch.zeros(4096, dtype=torch.uint8))
+    assert both([], [], [], [0]) == (None, None)
+    # every case below fails validation, so no HIP call is reached with the
+    # fake pointers
+    cases = [
+        (["a"], [0], [63], [0, 1]),          # token-major bytes are 2*1*2*2*4*2 = 64
+        (["a"], [0], [100], [0, 2]),         # two pages: 128
+        (["p"], [0], [64], [0, 1]),          # 3-D (MLA-like) layer, K only: 1*1*2*1*8*2 = 32
+        (["q"], [0], [16], [0, 1]),          # 2-D tensor: no token-major layout
+        (["b"], [0], [64], [0, 1]),
+        (["a"], [4090], [64], [0, 1]),
+    ]
+    for names, offs, sizes, io in cases:
+        e_c, e_o = both(names, offs, sizes, io)
+        assert e_o is not None and e_c == e_o, (names, sizes, e_c, e_o)
+    # the sizes the oracle accepts (checked on the oracle only)
+    for names, sizes, io in ((["a"], [64], [0, 1]), (["a"], [128], [0, 2]), (["p"], [32], [0, 1])):
+        assert oracle_error(lambda: ofn(names, [0], sizes, oidx, io)) is None
 
 
 def test_layout_errors_match_oracle(lib):

@@ -314,3 +314,55 @@ def test_selection_fuzz(dev, data):
     torch.cuda.synchronize()
     for t, td in zip(cpu, gpu):
         assert same_bytes(td, t)
+
+
+@FUZZ
+@given(data=st.data())
+def test_token_copies_fuzz(dev, data):
+    layout = data.draw(st.sampled_from(LAYOUTS), label="layout")
+    dtype = data.draw(st.sampled_from(DTYPES + [torch.float32]), label="dtype")
+    ps = data.draw(st.sampled_from([1, 3, 16]), label="page_size")
+    h = data.draw(st.sampled_from([1, 2, 3, 8]), label="heads")
+    d = data.draw(st.sampled_from([5, 16, 64, 128]), label="head_dim")
+    if layout == "packed" and dtype == torch.float32:
+        dtype = torch.bfloat16
+    nb = data.draw(st.integers(4, 30), label="num_blocks")
+    L = data.draw(st.integers(1, 3), label="layers")
+    seed = data.draw(st.integers(0, 2 ** 16), label="seed")
+    g = torch.Generator().manual_seed(seed)
+    layers = [make_layer(layout, nb, ps, h, d, dtype, g, kind="bytes") for _ in range(L)]
+    pf = layers[0][1]
+    n_kv = 1 if layout == "mla" else 2
+    chunks = _chunks(data, nb, ps)
+    names, offsets, sizes, flat, ioff = [], [], [], [], [0]
+    off = data.draw(st.sampled_from([0, 16, 4096, 5]), label="store base")
+    e = layers[0][0].element_size()
+    for pages, _, _ in chunks:
+        for li in range(L):
+            names.append(f"layer.{li}")
+            offsets.append(off)
+            sz = n_kv * len(pages) * ps * h * d * e
+            sizes.append(sz)
+            flat.extend(pages)
+            ioff.append(len(flat))
+            off += sz
+    store = torch.randint(0, 256, (off + 32,), dtype=torch.uint8, generator=g)
+    gather = data.draw(st.booleans(), label="gather")
+    oc, gc = OracleCopier(), cache_ops.CacheCopier()
+    dev_layers = []
+    for li, (t, _) in enumerate(layers):
+        oc.register_layer(f"layer.{li}", t, pf)
+        td = to_dev(t, dev)
+        dev_layers.append(td)
+        gc.register_layer(f"layer.{li}", td, pf)
+    oc.register_store(store.clone())
+    gstore = store.to(dev)
+    gc.register_store(gstore)
+    idx = torch.tensor(flat, dtype=torch.int32)
+    fn = "gather_tokens" if gather else "scatter_tokens"
+    getattr(oc, fn)(names, offsets, sizes, idx, ioff)
+    getattr(gc, fn)(names, offsets, sizes, idx.to(dev), ioff)
+    torch.cuda.synchronize()
+    assert torch.equal(gstore.cpu(), oc.store)
+    for (t, _), td in zip(layers, dev_layers):
+        assert same_bytes(td, t)

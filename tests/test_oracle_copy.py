@@ -169,3 +169,77 @@ def test_byte_view_offset():
     t = base[5:]
     mem, off = byte_view(t)
     assert off == 10 and mem[off] == 5
+
+
+def _elem(t, layout, kv, page, p, h, d):
+    """Element (kv, page, token p, head h, dim d) of a layer by explicit index
+    arithmetic on its logical shape (independent of the oracle's views)."""
+    if layout in ("nhd", "hnd"):          # logical [2, NB, PS, H, D]
+        return t[kv, page, p, h, d]
+    if layout in ("pf", "pf_hnd"):        # logical [NB, 2, PS, H, D]
+        return t[page, kv, p, h, d]
+    if layout == "packed":                # [NB, H, PS, 2D]
+        return t[page, h, p, kv * (t.shape[3] // 2) + d]
+    return t[page, p, d]                  # mla [NB, PS, hidden]
+
+
+@pytest.mark.parametrize("layout", ["nhd", "hnd", "pf", "pf_hnd", "packed", "mla"])
+def test_gather_tokens_brute_force_and_round_trip(layout):
+    from tests.gpu_util import make_layer
+    g = torch.Generator().manual_seed(21)
+    nb, ps, h, d = 9, 4, 3, 5
+    t, pf = make_layer(layout, nb, ps, h, d, torch.float16, g)
+    n_kv = 1 if layout == "mla" else 2
+    H, D = (1, h * d) if layout == "mla" else (h, d)
+    sel = [4, 0, 8, nb + 2, 2]                      # null and out-of-range pages are skipped
+    n = n_kv * len(sel) * ps * H * D * 2
+    base = torch.randint(0, 256, (n + 8,), dtype=torch.uint8, generator=g)
+    oc = OracleCopier()
+    oc.register_layer("x", t, pf)
+    oc.register_store(base.clone())
+    idx = torch.tensor(sel, dtype=torch.int32)
+    oc.gather_tokens(["x"], [8], [n], idx, [0, len(sel)])
+    out = oc.store[8:].view(torch.float16).view(n_kv, len(sel), ps, H, D)
+    keep = base[8:].view(torch.float16).view(n_kv, len(sel), ps, H, D)
+    for kv in range(n_kv):
+        for s, page in enumerate(sel):
+            for p in range(ps):
+                for hh in range(H):
+                    for dd in range(D):
+                        got = out[kv, s, p, hh, dd].view(torch.int16)
+                        if 0 < page < nb:
+                            want = _elem(t, layout, kv, page, p, hh, dd).view(torch.int16)
+                        else:
+                            want = keep[kv, s, p, hh, dd].view(torch.int16)
+                        assert int(got) == int(want), (kv, s, p, hh, dd)
+    assert torch.equal(oc.store[:8], base[:8])
+    # scatter_tokens of the gathered rows into a zeroed copy restores exactly
+    # the listed pages and leaves everything else zero
+    z = torch.zeros_like(t)
+    oc2 = OracleCopier()
+    oc2.register_layer("x", z, pf)
+    oc2.register_store(oc.store.clone())
+    oc2.scatter_tokens(["x"], [8], [n], idx, [0, len(sel)])
+    for page in range(nb):
+        for kv in range(n_kv):
+            for p in range(ps):
+                for hh in range(H):
+                    for dd in range(D):
+                        got = _elem(z, layout, kv, page, p, hh, dd).view(torch.int16)
+                        want = _elem(t, layout, kv, page, p, hh, dd).view(torch.int16) if page in (4, 8, 2) else 0
+                        assert int(got) == int(want), (page, kv, p, hh, dd)
+
+
+def test_gather_tokens_equals_gather_pages_for_nhd():
+    # vLLM's [2, NB, PS, H, D] pages are token-major already: both gathers agree
+    g = torch.Generator().manual_seed(22)
+    t = torch.randn(2, 12, 16, 4, 8, generator=g).to(torch.bfloat16)
+    sel = torch.tensor([3, 0, 11, 7], dtype=torch.int32)
+    n = 2 * 4 * 16 * 4 * 8 * 2
+    a, b = OracleCopier(), OracleCopier()
+    for c in (a, b):
+        c.register_layer("x", t, False)
+        c.register_store(torch.full((n,), 7, dtype=torch.uint8))
+    a.gather_pages(["x"], [0], [n], sel, [0, 4])
+    b.gather_tokens(["x"], [0], [n], sel, [0, 4])
+    assert torch.equal(a.store, b.store)
