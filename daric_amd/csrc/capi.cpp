@@ -419,7 +419,10 @@ int copy_tokens(daric_copier* c, const char* const* names, int64_t n_jobs, const
             const TokenLayout L = token_layout(t, layers[i]->page_first);
             const int64_t e = t.elem_size;
             const int64_t n_sel = indices_offsets[i + 1] - indices_offsets[i];
-            const int64_t num = L.n_kv * n_sel * L.PS * L.H * L.D * e;
+            const int64_t row = checked_multiply(checked_multiply(L.PS * L.H, L.D, "token-major rows"), e,
+                                                 "token-major rows");
+            const int64_t num = checked_multiply(checked_multiply(L.n_kv, n_sel, "token-major rows"), row,
+                                                 "token-major rows");
             if (byte_sizes[i] != num)
                 throw Error(DARIC_ERR_RUNTIME,
                             cat("byte_size mismatch at job ", i, " | C++ expected bytes: ", num,
