@@ -212,9 +212,23 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
         const int shift = 24 - 8 * pass;
         hist[tid] = 0;
         __syncthreads();
-        for (int i = tid; i < n; i += kThreads) {
-            const uint32_t key = s_keys[i];
-            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        // Lanes of a wavefront whose keys share a digit are found with eight
+        // ballots, and one of them adds the group's count: one LDS atomic per
+        // distinct digit instead of up to 64 colliding ones (the leading
+        // digits of one chunk's keys are nearly all equal).
+        for (int b = 0; b < n; b += kThreads) {
+            const int i = b + tid;
+            const uint32_t key = i < n ? s_keys[i] : 0u;
+            const bool act = i < n && (key & mask) == prefix;
+            const uint32_t dig = (key >> shift) & 255u;
+            unsigned long long same = __ballot(act);
+#pragma unroll
+            for (int bit = 0; bit < 8; ++bit) {
+                const unsigned long long ones = __ballot((dig >> bit) & 1u);
+                same &= ((dig >> bit) & 1u) ? ones : ~ones;
+            }
+            if (act && (tid & 63) == __ffsll(static_cast<long long>(same)) - 1)
+                atomicAdd(&hist[dig], static_cast<uint32_t>(__popcll(same)));
         }
         __syncthreads();
         // suffix sums over digits (from 255 down): thread t holds digit 255 - t
