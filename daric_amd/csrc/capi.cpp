@@ -1000,7 +1000,7 @@ int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_fi
                     (g.sh * ces) % need == 0 && aligned(t.data, need),
                     "kv_deviation needs head_dim % 8 == 0 and aligned K rows");
         for (int64_t i = 1; i < n_layers; ++i) DARIC_CHECK(aligned(layers[i].data, need), "misaligned layer ", i);
-        Chunks c = build_chunks(chunks, n_chunks, g.PS, numel(*block_table), T, 16);
+        Chunks c = build_chunks(chunks, n_chunks, g.PS, numel(*block_table), T, deviation_tile_tokens(ck));
         if (c.tiles == 0) return;
         DARIC_CHECK(c.tiles <= kMaxTiles, "too many tokens in one kv_deviation call");
         DeviceGuard guard(t.device);

@@ -81,7 +81,9 @@ void launch_rerotate_inplace(uint8_t* const* d_layers, int n_layers, const Inpla
                              const int32_t* block_table, const float* inv_freq, int kind,
                              bool neox, bool vec, hipStream_t stream);
 
-// Selection kernels.
+// Selection kernels. deviation_tile_tokens: tokens per deviation workgroup
+// (the tiling launch_deviation expects in SelChunk::tile_begin).
+int deviation_tile_tokens(int cache_kind);
 void launch_deviation(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int cache_kind,
                       const int32_t* block_table, const uint8_t* k_new, int new_kind,
                       int64_t T, const SelChunk* d_chunks, int n_chunks, int n_tiles,
