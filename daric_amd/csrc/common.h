@@ -94,9 +94,11 @@ public:
     };
     static DescRing& for_device(int device);
     // Copies `bytes` from `src` into a slot, enqueues the H2D copy on `stream`
-    // and returns the device address. The caller must call release() with
+    // and returns the device address. With `direct`, no copy is enqueued and
+    // the slot's pinned host address is returned: the kernels then read the
+    // descriptors over the host link. The caller must call release() with
     // the returned slot index after enqueueing every kernel that reads it.
-    void* upload(const void* src, size_t bytes, hipStream_t stream, int* slot_out);
+    void* upload(const void* src, size_t bytes, hipStream_t stream, int* slot_out, bool direct = false);
     void release(int slot, hipStream_t stream);
 
 private:
@@ -109,12 +111,13 @@ private:
     std::mutex mu_;
 };
 
-// RAII helper: uploads a descriptor array and releases its slot at scope exit.
+// RAII helper: uploads a descriptor array (or, with `direct`, hands out its
+// pinned host copy) and releases its slot at scope exit.
 class DescUpload {
 public:
-    DescUpload(int device, const void* src, size_t bytes, hipStream_t stream)
+    DescUpload(int device, const void* src, size_t bytes, hipStream_t stream, bool direct = false)
         : ring_(DescRing::for_device(device)), stream_(stream) {
-        ptr_ = ring_.upload(src, bytes, stream, &slot_);
+        ptr_ = ring_.upload(src, bytes, stream, &slot_, direct);
     }
     ~DescUpload() { ring_.release(slot_, stream_); }
     void* get() const { return ptr_; }

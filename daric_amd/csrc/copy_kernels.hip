@@ -147,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
 
     int jb, unit;
     block_unit<true>(njobs, jb, unit);
-    const CopyJob& j = jobs[jb];
+    const CopyJob j = jobs[jb];   // one read: the jobs may live in pinned host memory
     int p, s;
     uint8_t *cache, *stage;
     if (!resolve_tile(j, unit, p, s, cache, stage)) return;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
 
     int jb, unit;
     block_unit<true>(njobs, jb, unit);
-    const CopyJob& j = jobs[jb];
+    const CopyJob j = jobs[jb];   // one read: the jobs may live in pinned host memory
     int p, s;
     uint8_t *cache, *stage;
     if (!resolve_tile(j, unit, p, s, cache, stage)) return;

@@ -87,7 +87,7 @@ DescRing& DescRing::for_device(int device) {
     return *r;
 }
 
-void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* slot_out) {
+void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* slot_out, bool direct) {
     std::unique_lock<std::mutex> lk(mu_);
     // A slot between upload() and release() belongs to a call that is still
     // enqueueing kernels on it; skip such slots (wait if all are taken).
@@ -142,11 +142,14 @@ void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* s
     *slot_out = idx;
     try {
         std::memcpy(s.host, src, bytes);
-        // A kernel on `stream` copies the slot to the device. Unlike
-        // hipMemcpyAsync (a copy-engine transfer the compute queue must then
-        // wait for, ~17 us per call in a back-to-back pipeline on MI355X) it
-        // stays on the compute queue (~3 us). Slots are 16-byte multiples
-        // of at least 1 MiB, so the rounded copy stays in bounds.
+        // Direct: the kernels read the coherent pinned slot themselves; the
+        // event recorded at release() keeps the slot until they are done.
+        if (direct) return s.host;
+        // Otherwise a kernel on `stream` copies the slot to the device.
+        // Unlike hipMemcpyAsync (a copy-engine transfer the compute queue
+        // must then wait for, ~17 us per call in a back-to-back pipeline on
+        // MI355X) it stays on the compute queue (~3 us). Slots are 16-byte
+        // multiples of at least 1 MiB, so the rounded copy stays in bounds.
         launch_upload(s.host, s.dev, (bytes + 15) / 16, stream);
     } catch (...) {
         s.in_use = false;
