@@ -467,9 +467,9 @@ int copy_tokens(daric_copier* c, const char* const* names, int64_t n_jobs, const
         DARIC_CHECK(max_parts <= kMaxTiles, "too many pages in one job: ", max_parts);
         DeviceGuard guard(device);
         const hipStream_t st = as_stream(stream);
-        DescUpload up(device, jobs.data(), jobs.size() * sizeof(TokenJob), st);
-        launch_token_copy(static_cast<const TokenJob*>(up.get()), static_cast<int>(jobs.size()),
-                          static_cast<int>(max_parts), vw, lds, gather, st);
+        DescHandOver ho(device, jobs.data(), jobs.size() * sizeof(TokenJob), st);
+        launch_token_copy(ho.arg(), static_cast<int>(jobs.size()), static_cast<int>(max_parts), vw, lds,
+                          gather, st);
     });
 }
 
@@ -485,9 +485,9 @@ int copy_pages(daric_copier* c, const char* const* names, int64_t n_jobs, const 
         if (r.jobs.empty() || r.max_elements == 0) return;
         DeviceGuard guard(r.device);
         const hipStream_t st = as_stream(stream);
-        DescUpload up(r.device, r.jobs.data(), r.jobs.size() * sizeof(CopyJob), st);
-        launch_copy_pages(static_cast<const CopyJob*>(up.get()), static_cast<int>(r.jobs.size()),
-                          static_cast<int>(r.max_tiles), r.max_span, r.vw, gather, st);
+        DescHandOver ho(r.device, r.jobs.data(), r.jobs.size() * sizeof(CopyJob), st);
+        launch_copy_pages(ho.arg(), static_cast<int>(r.jobs.size()), static_cast<int>(r.max_tiles),
+                          r.max_span, r.vw, gather, st);
     });
 }
 
@@ -723,15 +723,15 @@ int daric_copier_scatter_pages_rerotate(daric_copier* c, const char* const* name
             gd.ipr = FastDiv(gd.g.ipr);
             gd.tok_div = FastDiv(gd.g.tok_div);
             gd.ps = FastDiv(gd.g.PS);
-            // The fused kernels read their job straight from the pinned slot
-            // (one 80-byte read per 32 KiB workgroup): no upload kernel and no
-            // dependency gap before them, ~4 us less per call on MI355X. The
-            // copy kernels keep the upload: their 8 KiB workgroups are 4x as
-            // many, and reading over the host link cost the gather ~5 us.
-            DescUpload up(r.device, gr.jobs.data(), gr.jobs.size() * sizeof(CopyJob), st, true);
-            launch_scatter_rotate(static_cast<const CopyJob*>(up.get()), static_cast<int>(gr.jobs.size()),
-                                  static_cast<int>(gr.max_tiles), gd, gr.kind, rope->is_neox != 0,
-                                  rope->inv_freq, st);
+            // Job sets too large to travel inline are read by the fused
+            // kernels straight from the pinned slot (one 80-byte read per
+            // 32 KiB workgroup): no upload kernel and no dependency gap before
+            // them, ~4 us less per call on MI355X. The copy kernels keep the
+            // upload: their 8 KiB workgroups are 4x as many, and reading over
+            // the host link cost the gather ~5 us.
+            DescHandOver ho(r.device, gr.jobs.data(), gr.jobs.size() * sizeof(CopyJob), st, true);
+            launch_scatter_rotate(ho.arg(), static_cast<int>(gr.jobs.size()), static_cast<int>(gr.max_tiles),
+                                  gd, gr.kind, rope->is_neox != 0, rope->inv_freq, st);
         }
     });
 }
@@ -894,10 +894,8 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
         std::memcpy(blob.data(), segs.data(), seg_bytes);
         const auto ptrs = layer_ptrs(layers, n_layers);
         std::memcpy(blob.data() + seg_bytes, ptrs.data(), n_layers * sizeof(uint8_t*));
-        DescUpload up(t.device, blob.data(), blob.size(), st);
-        const auto* d_segs = static_cast<const RopeSeg*>(up.get());
-        auto* const* d_layers = reinterpret_cast<uint8_t* const*>(static_cast<uint8_t*>(up.get()) + seg_bytes);
-        launch_rerotate_inplace(d_layers, static_cast<int>(n_layers), g, d_segs,
+        DescHandOver ho(t.device, blob.data(), blob.size(), st);
+        launch_rerotate_inplace(ho.arg(), static_cast<int>(seg_bytes), static_cast<int>(n_layers), g,
                                 static_cast<int>(segs.size()), static_cast<int>(tiles),
                                 static_cast<const int32_t*>(block_table->data), rope->inv_freq,
                                 kind, neox, vec, st);
@@ -1015,12 +1013,10 @@ int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_fi
         std::memcpy(blob.data(), c.v.data(), cb);
         const auto ptrs = layer_ptrs(layers, n_layers);
         std::memcpy(blob.data() + cb, ptrs.data(), n_layers * sizeof(uint8_t*));
-        DescUpload up(t.device, blob.data(), blob.size(), st);
-        auto* const* d_layers = reinterpret_cast<uint8_t* const*>(static_cast<uint8_t*>(up.get()) + cb);
-        launch_deviation(d_layers, static_cast<int>(n_layers), g, ck,
+        DescHandOver ho(t.device, blob.data(), blob.size(), st);
+        launch_deviation(ho.arg(), static_cast<int>(cb), static_cast<int>(n_layers), g, ck,
                          static_cast<const int32_t*>(block_table->data),
-                         static_cast<const uint8_t*>(k_new->data), nk, T,
-                         static_cast<const SelChunk*>(up.get()), static_cast<int>(c.v.size()),
+                         static_cast<const uint8_t*>(k_new->data), nk, T, static_cast<int>(c.v.size()),
                          static_cast<int>(c.tiles),
                          has_scales ? static_cast<const float*>(k_scales->data) : nullptr,
                          static_cast<float*>(keys->data), st);
@@ -1046,9 +1042,9 @@ int daric_topk_per_chunk(const daric_tensor* keys, const daric_chunk* chunks, in
         if (L == 0 || kmax == 0) return;
         DeviceGuard guard(keys->device);
         const hipStream_t st = as_stream(stream);
-        DescUpload up(keys->device, c.v.data(), c.v.size() * sizeof(SelChunk), st);
-        launch_topk(static_cast<const float*>(keys->data), static_cast<int>(L), T,
-                    static_cast<const SelChunk*>(up.get()), static_cast<int>(n_chunks),
+        DescHandOver ho(keys->device, c.v.data(), c.v.size() * sizeof(SelChunk), st);
+        launch_topk(static_cast<const float*>(keys->data), static_cast<int>(L), T, ho.arg(),
+                    static_cast<int>(n_chunks),
                     static_cast<int>(std::max<int64_t>(c.max_tokens, 1)),
                     static_cast<int32_t*>(out_idx->data), static_cast<int>(kmax), st);
     });
@@ -1089,14 +1085,13 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
         std::memcpy(blob.data(), c.v.data(), cb);
         const auto ptrs = layer_ptrs(layers, n_layers);
         std::memcpy(blob.data() + cb, ptrs.data(), n_layers * sizeof(uint8_t*));
-        DescUpload up(t.device, blob.data(), blob.size(), st);
-        auto* const* d_layers = reinterpret_cast<uint8_t* const*>(static_cast<uint8_t*>(up.get()) + cb);
-        launch_merge(d_layers, static_cast<int>(n_layers), g, t.elem_size,
+        DescHandOver ho(t.device, blob.data(), blob.size(), st);
+        launch_merge(ho.arg(), static_cast<int>(cb), static_cast<int>(n_layers), g, t.elem_size,
                      static_cast<const int32_t*>(block_table->data),
                      static_cast<const uint8_t*>(k_new->data),
                      g.v_off >= 0 ? static_cast<const uint8_t*>(v_new->data) : nullptr, T,
-                     static_cast<const SelChunk*>(up.get()), static_cast<int>(n_chunks),
-                     static_cast<const int32_t*>(sel_idx->data), static_cast<int>(kmax), st);
+                     static_cast<int>(n_chunks), static_cast<const int32_t*>(sel_idx->data),
+                     static_cast<int>(kmax), st);
     });
 }
 

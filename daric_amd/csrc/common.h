@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstring>
 #include <mutex>
+#include <optional>
 #include <sstream>
 #include <stdexcept>
 #include <string>
@@ -14,6 +15,7 @@
 #include <vector>
 
 #include "../../include/daric_cache_ops.h"
+#include "jobs.h"
 
 namespace daric {
 
@@ -127,6 +129,28 @@ private:
     hipStream_t stream_;
     int slot_ = -1;
     void* ptr_ = nullptr;
+};
+
+// Hands a call's descriptor bytes to its kernels: inline in the kernel
+// arguments when they fit (DescArg), else through the ring (an upload, or with
+// `direct` the pinned slot itself), released at scope exit.
+class DescHandOver {
+public:
+    DescHandOver(int device, const void* src, size_t bytes, hipStream_t stream, bool direct = false) {
+        arg_.ptr = nullptr;
+        arg_.reserved = 0;
+        if (bytes <= static_cast<size_t>(kInlineDescBytes)) {
+            if (bytes) std::memcpy(arg_.inl, src, bytes);
+        } else {
+            up_.emplace(device, src, bytes, stream, direct);
+            arg_.ptr = static_cast<const uint8_t*>(up_->get());
+        }
+    }
+    const DescArg& arg() const { return arg_; }
+
+private:
+    DescArg arg_;
+    std::optional<DescUpload> up_;
 };
 
 // Sets the current device for the scope and restores the previous one.

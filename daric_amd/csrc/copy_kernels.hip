@@ -106,11 +106,11 @@ __device__ __forceinline__ void block_unit(const FastDiv& njobs, int& job, int& 
 }
 
 template <int VW, bool GATHER, bool JOB_MINOR>
-__global__ __launch_bounds__(kThreads) void copy_pages_kernel(const CopyJob* __restrict__ jobs,
-                                                              FastDiv njobs, int log2_parts) {
+__global__ __launch_bounds__(kThreads) void copy_pages_kernel(DescArg d, int job0, FastDiv njobs,
+                                                              int log2_parts) {
     int jb, unit;
     block_unit<JOB_MINOR>(njobs, jb, unit);
-    const CopyJob& j = jobs[jb];
+    const CopyJob j = desc_load(desc_at<CopyJob>(d, 0) + job0 + jb);
     int p, s;
     uint8_t *cache, *stage;
     if (!resolve_tile(j, unit >> log2_parts, p, s, cache, stage)) return;
@@ -138,8 +138,7 @@ __global__ __launch_bounds__(kThreads) void copy_pages_kernel(const CopyJob* __r
 // cancels in a linear rotation.
 template <int KIND, bool NEOX>
 __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
-    const CopyJob* __restrict__ jobs, FastDiv njobs, RowGeomDiv gd,
-    const float* __restrict__ inv_freq) {
+    DescArg d, int job0, FastDiv njobs, RowGeomDiv gd, const float* __restrict__ inv_freq) {
     using E = Elem<KIND>;
     constexpr int VE = E::VE;
     __shared__ float s_cos[kMaxHalfRot];
@@ -147,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
 
     int jb, unit;
     block_unit<true>(njobs, jb, unit);
-    const CopyJob j = jobs[jb];   // one read: the jobs may live in pinned host memory
+    const CopyJob j = desc_load(desc_at<CopyJob>(d, 0) + job0 + jb);
     int p, s;
     uint8_t *cache, *stage;
     if (!resolve_tile(j, unit, p, s, cache, stage)) return;
@@ -265,8 +264,7 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
 #endif
 template <int KIND, bool NEOX>
 __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
-    const CopyJob* __restrict__ jobs, FastDiv njobs, RowGeomDiv gd,
-    const float* __restrict__ inv_freq) {
+    DescArg d, int job0, FastDiv njobs, RowGeomDiv gd, const float* __restrict__ inv_freq) {
     using E = Elem<KIND>;
     constexpr int VE = E::VE;
     constexpr int EPW = E::EPW;
@@ -277,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
 
     int jb, unit;
     block_unit<true>(njobs, jb, unit);
-    const CopyJob j = jobs[jb];   // one read: the jobs may live in pinned host memory
+    const CopyJob j = desc_load(desc_at<CopyJob>(d, 0) + job0 + jb);
     int p, s;
     uint8_t *cache, *stage;
     if (!resolve_tile(j, unit, p, s, cache, stage)) return;
@@ -384,7 +382,7 @@ __global__ __launch_bounds__(kThreads) void upload_kernel(const u32x4* __restric
 constexpr int64_t kMaxBlocksX = (1ll << 24) - 1;
 constexpr int kMaxY = 65535;
 
-void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int64_t max_span, int vw,
+void launch_copy_pages(const DescArg& d, int n_jobs, int max_tiles, int64_t max_span, int vw,
                        bool gather, hipStream_t stream) {
     // tiles cut into parts of about 8 KiB
     int log2_parts = 0;
@@ -399,10 +397,9 @@ void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int64_t
             const int nj = std::min(slice, n_jobs - j0);
             const FastDiv fd(static_cast<uint32_t>(nj));
             const dim3 grid(static_cast<unsigned>(units * nj));
-            const CopyJob* jp = d_jobs + j0;
-            if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, false, true>), grid, kThreads, 0, stream, jp, fd, log2_parts);
-            else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, false, true>), grid, kThreads, 0, stream, jp, fd, log2_parts);
-            else DARIC_LAUNCH((copy_pages_kernel<1, false, true>), grid, kThreads, 0, stream, jp, fd, log2_parts);
+            if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, false, true>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
+            else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, false, true>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
+            else DARIC_LAUNCH((copy_pages_kernel<1, false, true>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
             check_launch("scatter_pages");
         }
         return;
@@ -413,10 +410,9 @@ void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int64_t
         const int nj = std::min(kMaxY, n_jobs - j0);
         const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(max_tiles) << log2_parts),
                         static_cast<unsigned>(nj));
-        const CopyJob* jp = d_jobs + j0;
-        if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, true, false>), grid, kThreads, 0, stream, jp, fd, log2_parts);
-        else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, true, false>), grid, kThreads, 0, stream, jp, fd, log2_parts);
-        else DARIC_LAUNCH((copy_pages_kernel<1, true, false>), grid, kThreads, 0, stream, jp, fd, log2_parts);
+        if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, true, false>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
+        else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, true, false>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
+        else DARIC_LAUNCH((copy_pages_kernel<1, true, false>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
         check_launch("gather_pages");
     }
 }
@@ -429,7 +425,7 @@ void launch_upload(const void* src, void* dst, size_t n16, hipStream_t stream) {
     check_launch("descriptor upload");
 }
 
-void launch_scatter_rotate(const CopyJob* d_jobs, int n_jobs, int max_tiles,
+void launch_scatter_rotate(const DescArg& d, int n_jobs, int max_tiles,
                            const RowGeomDiv& geom, int kind, bool neox, const float* inv_freq,
                            hipStream_t stream) {
     // the lane-exchange kernel needs whole rows inside a wavefront
@@ -441,15 +437,14 @@ void launch_scatter_rotate(const CopyJob* d_jobs, int n_jobs, int max_tiles,
         const int nj = std::min(slice, n_jobs - j0);
         const FastDiv fd(static_cast<uint32_t>(nj));
         const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(max_tiles) * nj));
-        const CopyJob* jp = d_jobs + j0;
         if (lane) {
-#define DARIC_SR(K, N) DARIC_LAUNCH((scatter_rotate_lane_kernel<K, N>), grid, kThreads, 0, stream, jp, fd, geom, inv_freq)
+#define DARIC_SR(K, N) DARIC_LAUNCH((scatter_rotate_lane_kernel<K, N>), grid, kThreads, 0, stream, d, j0, fd, geom, inv_freq)
             if (kind == kBF16) { if (neox) DARIC_SR(kBF16, true); else DARIC_SR(kBF16, false); }
             else if (kind == kF16) { if (neox) DARIC_SR(kF16, true); else DARIC_SR(kF16, false); }
             else { if (neox) DARIC_SR(kE4M3, true); else DARIC_SR(kE4M3, false); }
 #undef DARIC_SR
         } else {
-#define DARIC_SR(K, N) DARIC_LAUNCH((scatter_rotate_kernel<K, N>), grid, kThreads, 0, stream, jp, fd, geom, inv_freq)
+#define DARIC_SR(K, N) DARIC_LAUNCH((scatter_rotate_kernel<K, N>), grid, kThreads, 0, stream, d, j0, fd, geom, inv_freq)
             if (kind == kBF16) { if (neox) DARIC_SR(kBF16, true); else DARIC_SR(kBF16, false); }
             else if (kind == kF16) { if (neox) DARIC_SR(kF16, true); else DARIC_SR(kF16, false); }
             else { if (neox) DARIC_SR(kE4M3, true); else DARIC_SR(kE4M3, false); }

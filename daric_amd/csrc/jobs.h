@@ -5,6 +5,48 @@
 
 namespace daric {
 
+// Hand-over of a call's descriptors (jobs, segments, chunks, layer pointer
+// tables) to its kernels. Descriptors of up to kInlineDescBytes travel inline
+// in the kernel arguments (`ptr` null): no descriptor copy, no ring slot and
+// no completion event, ~4 us per call on MI355X against ~9 us through the
+// ring; such a launch also carries its descriptors by value, as a captured
+// graph node needs. Larger sets go through the descriptor ring and `ptr`
+// points at them (device memory, or the pinned host slot itself).
+constexpr int kInlineDescBytes = 2816;
+struct alignas(16) DescArg {
+    const uint8_t* ptr;
+    uint64_t reserved;
+    alignas(16) uint8_t inl[kInlineDescBytes];
+#ifdef __HIPCC__
+    __host__ __device__
+#endif
+    const uint8_t* base() const { return ptr != nullptr ? ptr : inl; }
+};
+
+#ifdef __HIPCC__
+// Descriptors are read-only and uniform across a workgroup: kernels address
+// them in the constant address space, so they load through the scalar unit
+// into SGPRs (a generic pointer would put them in VGPRs).
+template <typename T>
+using DescPtr = const __attribute__((address_space(4))) T*;
+template <typename T>
+__device__ __forceinline__ DescPtr<T> desc_at(const DescArg& d, int byte_off) {
+    return (DescPtr<T>)(d.base() + byte_off);
+}
+// Copies one descriptor out of the constant address space, word by word.
+template <typename T>
+__device__ __forceinline__ T desc_load(DescPtr<T> p) {
+    static_assert(sizeof(T) % 4 == 0, "descriptors are whole 32-bit words");
+    T v;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(&v);
+    const __attribute__((address_space(4))) uint32_t* src =
+        reinterpret_cast<const __attribute__((address_space(4))) uint32_t*>(p);
+#pragma unroll
+    for (unsigned i = 0; i < sizeof(T) / 4; ++i) dst[i] = src[i];
+    return v;
+}
+#endif
+
 // One page-copy job: one (layer, chunk) pair, the counterpart of the
 // reference's PageCopyJobDesc (csrc/cache_ops/cache_ops.h:24-36). Byte units.
 // Tile t of the job (t < prefix * n_sel) is prefix index p = t / n_sel and

@@ -59,41 +59,43 @@ static_assert(sizeof(TokenJob) == 112, "TokenJob layout");
 
 // Token-major gather (staging <- cache) or scatter; lds selects the
 // LDS-staged transpose for head-major pages ([H, PS, D] dense); vw is 16 or 1.
-void launch_token_copy(const TokenJob* d_jobs, int n_jobs, int max_parts, int vw, bool lds,
+void launch_token_copy(const DescArg& d, int n_jobs, int max_parts, int vw, bool lds,
                        bool gather, hipStream_t stream);
 
-// Plain page copies. vw is the access width in bytes (16, 4 or 1); max_span
+// Plain page copies of the n_jobs CopyJobs in `d`. vw is the access width in
+// bytes (16, 4 or 1); max_span
 // is the largest page span (bytes) of the jobs.
-void launch_copy_pages(const CopyJob* d_jobs, int n_jobs, int max_tiles, int64_t max_span, int vw,
+void launch_copy_pages(const DescArg& d, int n_jobs, int max_tiles, int64_t max_span, int vw,
                        bool gather, hipStream_t stream);
 
-// Fused scatter + K re-rotation; kind is an ElemKind. All jobs share `geom`.
-void launch_scatter_rotate(const CopyJob* d_jobs, int n_jobs, int max_tiles,
+// Fused scatter + K re-rotation of the n_jobs CopyJobs in `d`; kind is an
+// ElemKind. All jobs share `geom`.
+void launch_scatter_rotate(const DescArg& d, int n_jobs, int max_tiles,
                            const RowGeomDiv& geom, int kind, bool neox, const float* inv_freq,
                            hipStream_t stream);
 
-// In-place K re-rotation over segments of tokens. `layers` is a device array
-// of n_layers K base pointers; `vec` selects 16-byte (true) or per-element
-// (false) access. fp8 codes are rotated as stored (a per-head scale cancels
-// in a linear rotation).
-void launch_rerotate_inplace(uint8_t* const* d_layers, int n_layers, const InplaceGeom& g,
-                             const RopeSeg* d_segs, int n_segs, int n_tiles,
-                             const int32_t* block_table, const float* inv_freq, int kind,
-                             bool neox, bool vec, hipStream_t stream);
+// In-place K re-rotation over segments of tokens. `d` holds the n_segs
+// RopeSegs, then (at byte layer_off) the n_layers K base pointers; `vec`
+// selects 16-byte (true) or per-element (false) access. fp8 codes are
+// rotated as stored (a per-head scale cancels in a linear rotation).
+void launch_rerotate_inplace(const DescArg& d, int layer_off, int n_layers, const InplaceGeom& g,
+                             int n_segs, int n_tiles, const int32_t* block_table,
+                             const float* inv_freq, int kind, bool neox, bool vec, hipStream_t stream);
 
 // Selection kernels. deviation_tile_tokens: tokens per deviation workgroup
 // (the tiling launch_deviation expects in SelChunk::tile_begin).
 int deviation_tile_tokens(int cache_kind);
-void launch_deviation(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int cache_kind,
+// Selection launchers: `d` holds the n_chunks SelChunks, then (deviation and
+// merge, at byte layer_off) the n_layers layer base pointers.
+void launch_deviation(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int cache_kind,
                       const int32_t* block_table, const uint8_t* k_new, int new_kind,
-                      int64_t T, const SelChunk* d_chunks, int n_chunks, int n_tiles,
+                      int64_t T, int n_chunks, int n_tiles,
                       const float* k_scales, float* keys, hipStream_t stream);
-void launch_topk(const float* keys, int n_layers, int64_t T, const SelChunk* d_chunks,
+void launch_topk(const float* keys, int n_layers, int64_t T, const DescArg& d,
                  int n_chunks, int max_tokens, int32_t* out_idx, int kmax, hipStream_t stream);
-void launch_merge(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int elem_size,
+void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int elem_size,
                   const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,
-                  int64_t T, const SelChunk* d_chunks, int n_chunks, const int32_t* sel_idx,
-                  int kmax, hipStream_t stream);
+                  int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, hipStream_t stream);
 
 // Copies n16 16-byte units from host-pinned `src` to device `dst` on `stream`
 // (descriptor upload; both 16-byte aligned).

@@ -23,7 +23,7 @@ constexpr int kThreads = 256;
 constexpr int kVecUnroll = 2;
 constexpr int kMaxHalfRot = 256;
 
-__device__ __forceinline__ int find_segment(const RopeSeg* __restrict__ segs, int n, int tile) {
+__device__ __forceinline__ int find_segment(DescPtr<RopeSeg> segs, int n, int tile) {
     int lo = 0, hi = n - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -52,8 +52,8 @@ __device__ __forceinline__ void fill_cos_sin(float* s_cos, float* s_sin, int hal
 // positive per-head scale s gives rot(q * s) / s = rot(q) and cancels.
 template <int KIND, bool NEOX>
 __global__ __launch_bounds__(kThreads) void rerotate_vec_kernel(
-    uint8_t* const* __restrict__ layers, InplaceGeom g, const RopeSeg* __restrict__ segs,
-    int n_segs, const int32_t* __restrict__ bt, const float* __restrict__ inv_freq,
+    DescArg d, int layer_off, int layer0, InplaceGeom g, int n_segs,
+    const int32_t* __restrict__ bt, const float* __restrict__ inv_freq,
     FastDiv d_tok, FastDiv d_rot, FastDiv d_ps) {
     using E = Elem<KIND>;
     constexpr int VE = E::VE;
@@ -61,8 +61,10 @@ __global__ __launch_bounds__(kThreads) void rerotate_vec_kernel(
     __shared__ float s_cos[kMaxHalfRot];
     __shared__ float s_sin[kMaxHalfRot];
 
+    const DescPtr<RopeSeg> segs = desc_at<RopeSeg>(d, 0);
+    const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off) + layer0;
     const int tile = static_cast<int>(blockIdx.x);
-    const RopeSeg& sg = segs[find_segment(segs, n_segs, tile)];
+    const RopeSeg sg = desc_load(segs + find_segment(segs, n_segs, tile));
     const int tok0 = (tile - sg.tile_begin) * g.tile_tokens;
     const int n_tok = min(g.tile_tokens, sg.n_tokens - tok0);
     if (n_tok <= 0 || sg.delta == 0.0f) return;
@@ -151,13 +153,15 @@ __device__ __forceinline__ void store_elem(uint8_t* p, float v) {
 
 template <int KIND, bool NEOX>
 __global__ __launch_bounds__(kThreads) void rerotate_elem_kernel(
-    uint8_t* const* __restrict__ layers, InplaceGeom g, const RopeSeg* __restrict__ segs,
-    int n_segs, const int32_t* __restrict__ bt, const float* __restrict__ inv_freq) {
+    DescArg d, int layer_off, int layer0, InplaceGeom g, int n_segs,
+    const int32_t* __restrict__ bt, const float* __restrict__ inv_freq) {
     constexpr int ES = KIND == kE4M3 ? 1 : 2;
     __shared__ float s_cos[kMaxHalfRot];
     __shared__ float s_sin[kMaxHalfRot];
+    const DescPtr<RopeSeg> segs = desc_at<RopeSeg>(d, 0);
+    const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off) + layer0;
     const int tile = static_cast<int>(blockIdx.x);
-    const RopeSeg& sg = segs[find_segment(segs, n_segs, tile)];
+    const RopeSeg sg = desc_load(segs + find_segment(segs, n_segs, tile));
     const int tok0 = (tile - sg.tile_begin) * g.tile_tokens;
     const int n_tok = min(g.tile_tokens, sg.n_tokens - tok0);
     if (n_tok <= 0 || sg.delta == 0.0f) return;
@@ -188,19 +192,17 @@ __global__ __launch_bounds__(kThreads) void rerotate_elem_kernel(
 
 }  // namespace
 
-void launch_rerotate_inplace(uint8_t* const* d_layers, int n_layers, const InplaceGeom& g,
-                             const RopeSeg* d_segs, int n_segs, int n_tiles,
-                             const int32_t* block_table, const float* inv_freq, int kind,
-                             bool neox, bool vec, hipStream_t stream) {
+void launch_rerotate_inplace(const DescArg& d, int layer_off, int n_layers, const InplaceGeom& g,
+                             int n_segs, int n_tiles, const int32_t* block_table,
+                             const float* inv_freq, int kind, bool neox, bool vec, hipStream_t stream) {
     constexpr int kMaxY = 65535;
     const FastDiv d_tok(static_cast<uint32_t>(g.H * g.n_rot)), d_rot(static_cast<uint32_t>(g.n_rot)),
         d_ps(static_cast<uint32_t>(g.PS));
     for (int l0 = 0; l0 < n_layers; l0 += kMaxY) {
         const int nl = n_layers - l0 < kMaxY ? n_layers - l0 : kMaxY;
         const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(nl));
-        uint8_t* const* lp = d_layers + l0;
-#define DARIC_RV(K, N) DARIC_LAUNCH((rerotate_vec_kernel<K, N>), grid, kThreads, 0, stream, lp, g, d_segs, n_segs, block_table, inv_freq, d_tok, d_rot, d_ps)
-#define DARIC_RE(K, N) DARIC_LAUNCH((rerotate_elem_kernel<K, N>), grid, kThreads, 0, stream, lp, g, d_segs, n_segs, block_table, inv_freq)
+#define DARIC_RV(K, N) DARIC_LAUNCH((rerotate_vec_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq, d_tok, d_rot, d_ps)
+#define DARIC_RE(K, N) DARIC_LAUNCH((rerotate_elem_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq)
         if (vec) {
             if (kind == kBF16) { if (neox) DARIC_RV(kBF16, true); else DARIC_RV(kBF16, false); }
             else if (kind == kF16) { if (neox) DARIC_RV(kF16, true); else DARIC_RV(kF16, false); }

@@ -31,7 +31,7 @@ constexpr int kWaves = kThreads / 64;
 template <int CK> constexpr int dev_tok_per_wave() { return CK == kE4M3 ? 4 : 8; }
 constexpr int kMergeTok = 8;                       // selected tokens per merge workgroup
 
-__device__ __forceinline__ int find_chunk(const SelChunk* __restrict__ ch, int n, int tile) {
+__device__ __forceinline__ int find_chunk(DescPtr<SelChunk> ch, int n, int tile) {
     int lo = 0, hi = n - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -84,14 +84,16 @@ __device__ __forceinline__ void unpack8(const Raw8<KIND>& r, float* x, float sca
 
 template <int CK, int NK>
 __global__ __launch_bounds__(kThreads) void deviation_kernel(
-    uint8_t* const* __restrict__ layers, KVGeom g, const int32_t* __restrict__ bt,
-    const uint8_t* __restrict__ k_new, int64_t T, const SelChunk* __restrict__ chunks,
-    int n_chunks, const float* __restrict__ k_scales, float* __restrict__ keys) {
+    DescArg d, int layer_off, KVGeom g, const int32_t* __restrict__ bt,
+    const uint8_t* __restrict__ k_new, int64_t T, int n_chunks,
+    const float* __restrict__ k_scales, float* __restrict__ keys) {
 #pragma clang fp contract(off)
+    const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
+    const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
     constexpr int CES = CK == kE4M3 ? 1 : 2;
     const int l = static_cast<int>(blockIdx.y);
     const int tile = static_cast<int>(blockIdx.x);
-    const SelChunk& c = chunks[find_chunk(chunks, n_chunks, tile)];
+    const SelChunk c = desc_load(chunks + find_chunk(chunks, n_chunks, tile));
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     constexpr int kTokPerWave = dev_tok_per_wave<CK>();
@@ -190,9 +192,9 @@ __device__ __forceinline__ int block_excl_count(bool flag, int* s_wave, int* tot
 }
 
 __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ keys, int64_t T,
-                                                        const SelChunk* __restrict__ chunks,
-                                                        int n_chunks, int32_t* __restrict__ out,
-                                                        int kmax) {
+                                                        DescArg d, int n_chunks,
+                                                        int32_t* __restrict__ out, int kmax) {
+    const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     extern __shared__ uint32_t s_keys[];
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_digit, s_above;
@@ -200,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
 
     const int l = static_cast<int>(blockIdx.y);
     const int ci = static_cast<int>(blockIdx.x);
-    const SelChunk& c = chunks[ci];
+    const SelChunk c = desc_load(chunks + ci);
     const int n = c.n_tokens;
     const int k = min(max(c.k, 0), n);
     int32_t* __restrict__ orow = out + (static_cast<int64_t>(l) * n_chunks + ci) * kmax;
@@ -282,13 +284,15 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
 
 template <int VW>
 __global__ __launch_bounds__(kThreads) void merge_kernel(
-    uint8_t* const* __restrict__ layers, KVGeom g, int es, const int32_t* __restrict__ bt,
+    DescArg d, int layer_off, KVGeom g, int es, const int32_t* __restrict__ bt,
     const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T,
-    const SelChunk* __restrict__ chunks, int n_chunks, const int32_t* __restrict__ sel, int kmax) {
+    int n_chunks, const int32_t* __restrict__ sel, int kmax) {
+    const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
+    const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
     using V = typename std::conditional<VW == 16, u32x4, uint8_t>::type;
     const int l = static_cast<int>(blockIdx.z);
     const int ci = static_cast<int>(blockIdx.y);
-    const SelChunk& c = chunks[ci];
+    const SelChunk c = desc_load(chunks + ci);
     const int q0 = static_cast<int>(blockIdx.x) * kMergeTok;
     const int32_t* srow = sel + (static_cast<int64_t>(l) * n_chunks + ci) * kmax;
     uint8_t* __restrict__ base = layers[l];
@@ -329,13 +333,14 @@ constexpr int kRowTok = 2;
 constexpr int kRowUnits = 4;   // 16-byte units per lane per row (rows <= 4 KiB)
 
 __global__ __launch_bounds__(kThreads) void merge_rows_kernel(
-    uint8_t* const* __restrict__ layers, KVGeom g, int es, const int32_t* __restrict__ bt,
+    DescArg d, int layer_off, KVGeom g, int es, const int32_t* __restrict__ bt,
     const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T,
-    const SelChunk* __restrict__ chunks, int n_chunks, const int32_t* __restrict__ sel, int kmax,
-    FastDiv d_upr) {
+    int n_chunks, const int32_t* __restrict__ sel, int kmax, FastDiv d_upr) {
+    const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
+    const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
     const int l = static_cast<int>(blockIdx.z);
     const int ci = static_cast<int>(blockIdx.y);
-    const SelChunk& c = chunks[ci];
+    const SelChunk c = desc_load(chunks + ci);
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int q0 = (static_cast<int>(blockIdx.x) * kWaves + wave) * kRowTok;
@@ -390,12 +395,12 @@ int deviation_tile_tokens(int cache_kind) {
     return kWaves * (cache_kind == kE4M3 ? dev_tok_per_wave<kE4M3>() : dev_tok_per_wave<kBF16>());
 }
 
-void launch_deviation(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int cache_kind,
+void launch_deviation(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int cache_kind,
                       const int32_t* block_table, const uint8_t* k_new, int new_kind,
-                      int64_t T, const SelChunk* d_chunks, int n_chunks, int n_tiles,
+                      int64_t T, int n_chunks, int n_tiles,
                       const float* k_scales, float* keys, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_layers));
-#define DARIC_DV(C, N) DARIC_LAUNCH((deviation_kernel<C, N>), grid, kThreads, 0, stream, d_layers, g, block_table, k_new, T, d_chunks, n_chunks, k_scales, keys)
+#define DARIC_DV(C, N) DARIC_LAUNCH((deviation_kernel<C, N>), grid, kThreads, 0, stream, d, layer_off, g, block_table, k_new, T, n_chunks, k_scales, keys)
     if (new_kind == kBF16) {
         if (cache_kind == kBF16) DARIC_DV(kBF16, kBF16);
         else if (cache_kind == kF16) DARIC_DV(kF16, kBF16);
@@ -409,18 +414,17 @@ void launch_deviation(uint8_t* const* d_layers, int n_layers, const KVGeom& g, i
     check_launch("kv_deviation");
 }
 
-void launch_topk(const float* keys, int n_layers, int64_t T, const SelChunk* d_chunks,
+void launch_topk(const float* keys, int n_layers, int64_t T, const DescArg& d,
                  int n_chunks, int max_tokens, int32_t* out_idx, int kmax, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
     const size_t lds = static_cast<size_t>(max_tokens) * sizeof(uint32_t);
-    DARIC_LAUNCH((topk_kernel), grid, kThreads, lds, stream, keys, T, d_chunks, n_chunks, out_idx, kmax);
+    DARIC_LAUNCH((topk_kernel), grid, kThreads, lds, stream, keys, T, d, n_chunks, out_idx, kmax);
     check_launch("topk_per_chunk");
 }
 
-void launch_merge(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int elem_size,
+void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int elem_size,
                   const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,
-                  int64_t T, const SelChunk* d_chunks, int n_chunks, const int32_t* sel_idx,
-                  int kmax, hipStream_t stream) {
+                  int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((kmax + kMergeTok - 1) / kMergeTok),
                     static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
     const bool vec = (g.D * elem_size) % 16 == 0 && (g.sb * elem_size) % 16 == 0 &&
@@ -430,14 +434,14 @@ void launch_merge(uint8_t* const* d_layers, int n_layers, const KVGeom& g, int e
     if (vec && g.H * upr <= 64 * kRowUnits) {
         const dim3 rgrid(static_cast<unsigned>((kmax + kWaves * kRowTok - 1) / (kWaves * kRowTok)),
                          static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
-        DARIC_LAUNCH((merge_rows_kernel), rgrid, kThreads, 0, stream, d_layers, g, elem_size, block_table,
-                     k_new, v_new, T, d_chunks, n_chunks, sel_idx, kmax, FastDiv(static_cast<uint32_t>(upr)));
+        DARIC_LAUNCH((merge_rows_kernel), rgrid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
+                     k_new, v_new, T, n_chunks, sel_idx, kmax, FastDiv(static_cast<uint32_t>(upr)));
     } else if (vec)
-        DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d_layers, g, elem_size, block_table, k_new,
-                                                        v_new, T, d_chunks, n_chunks, sel_idx, kmax);
+        DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table, k_new,
+                     v_new, T, n_chunks, sel_idx, kmax);
     else
-        DARIC_LAUNCH((merge_kernel<1>), grid, kThreads, 0, stream, d_layers, g, elem_size, block_table, k_new,
-                                                       v_new, T, d_chunks, n_chunks, sel_idx, kmax);
+        DARIC_LAUNCH((merge_kernel<1>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table, k_new,
+                     v_new, T, n_chunks, sel_idx, kmax);
     check_launch("merge_rows");
 }
 
