@@ -58,8 +58,12 @@ def _ext_stream(stream: int, device: torch.device):
 
 def _record(stream: int, device: torch.device, *tensors) -> None:
     """Keep caching-allocator memory of temporaries alive until `stream` has
-    consumed them (the reference's record_tensor_on_external_stream)."""
+    consumed them (the reference's record_tensor_on_external_stream). Not
+    while a graph is being captured: a captured graph's inputs must outlive
+    its replays, which is the caller's to ensure, as for any graph."""
     if device is None or device.type != "cuda":
+        return
+    if torch.cuda.is_current_stream_capturing():
         return
     ext = _ext_stream(stream, device)
     for t in tensors:

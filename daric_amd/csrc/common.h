@@ -142,6 +142,13 @@ public:
         if (bytes <= static_cast<size_t>(kInlineDescBytes)) {
             if (bytes) std::memcpy(arg_.inl, src, bytes);
         } else {
+            // The ring's slots are rewritten by later calls, so a graph node
+            // pointing at one would replay stale descriptors: refuse capture.
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+                throw Error(DARIC_ERR_INVALID,
+                            cat("this call's descriptors (", bytes, " bytes) exceed the ", kInlineDescBytes,
+                                " bytes that travel in kernel arguments; it cannot be captured in a graph"));
             up_.emplace(device, src, bytes, stream, direct);
             arg_.ptr = static_cast<const uint8_t*>(up_->get());
         }

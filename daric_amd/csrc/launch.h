@@ -1,9 +1,10 @@
-// Kernel launch wrapper shared by the .hip files. Every launch goes through
-// hipExtLaunchKernelGGL so that, when kernel timing is enabled
-// (daric_timing_enable), the dispatch packet itself records start/stop
-// timestamps: the measured interval is the kernel's execution, the same
-// interval rocprofv3 reports, without the gap an event recorded before and
-// after the launch on the stream would add.
+// Kernel launch wrapper shared by the .hip files. When kernel timing is
+// enabled (daric_timing_enable) a launch goes through hipExtLaunchKernelGGL,
+// so that the dispatch packet itself records start/stop timestamps: the
+// measured interval is the kernel's execution, the same interval rocprofv3
+// reports, without the gap an event recorded before and after the launch on
+// the stream would add. Otherwise it is a plain launch, which is also what a
+// stream capture records into a graph.
 #pragma once
 
 #include <hip/hip_ext.h>
@@ -22,7 +23,13 @@ void timing_record(hipEvent_t start, hipEvent_t stop);
     do {                                                                                      \
         hipEvent_t daric_ev0_ = nullptr, daric_ev1_ = nullptr;                               \
         ::daric::timing_events(&daric_ev0_, &daric_ev1_);                                     \
-        hipExtLaunchKernelGGL(kern, dim3(grid), dim3(block), static_cast<std::uint32_t>(shmem), \
-                              stream, daric_ev0_, daric_ev1_, 0, __VA_ARGS__);                \
-        ::daric::timing_record(daric_ev0_, daric_ev1_);                                       \
+        if (daric_ev0_ != nullptr) {                                                          \
+            hipExtLaunchKernelGGL(kern, dim3(grid), dim3(block), static_cast<std::uint32_t>(shmem), \
+                                  stream, daric_ev0_, daric_ev1_, 0, __VA_ARGS__);            \
+            ::daric::timing_record(daric_ev0_, daric_ev1_);                                   \
+        } else {                                                                              \
+            /* plain launch: the form graph capture records */                               \
+            hipLaunchKernelGGL(kern, dim3(grid), dim3(block), static_cast<std::uint32_t>(shmem), \
+                               stream, __VA_ARGS__);                                          \
+        }                                                                                     \
     } while (0)
