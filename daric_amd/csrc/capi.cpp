@@ -448,7 +448,7 @@ int copy_tokens(daric_copier* c, const char* const* names, int64_t n_jobs, const
                   j.row_bytes >= 128 && static_cast<int64_t>(j.H) * (j.row_bytes / 16) <= 512;
         }
         const int vw = vec ? 16 : 1;
-        int64_t max_parts = 0;
+        int64_t max_parts = 0, part_bytes = 0;
         for (TokenJob& j : jobs) {
             const int64_t row_units = j.row_bytes / vw;
             const int64_t head_units = static_cast<int64_t>(j.H) * row_units;
@@ -462,14 +462,15 @@ int copy_tokens(daric_copier* c, const char* const* names, int64_t n_jobs, const
             j.d_h = FastDiv(static_cast<uint32_t>(j.H));
             DARIC_CHECK(pt * head_units <= kIntMax, "page part exceeds int range");
             max_parts = std::max<int64_t>(max_parts, static_cast<int64_t>(j.n_kv) * j.n_sel * j.parts_per_page);
+            part_bytes = std::max<int64_t>(part_bytes, pt * j.H * j.row_bytes);
         }
         if (max_parts == 0) return;
         DARIC_CHECK(max_parts <= kMaxTiles, "too many pages in one job: ", max_parts);
         DeviceGuard guard(device);
         const hipStream_t st = as_stream(stream);
         DescHandOver ho(device, jobs.data(), jobs.size() * sizeof(TokenJob), st);
-        launch_token_copy(ho.arg(), static_cast<int>(jobs.size()), static_cast<int>(max_parts), vw, lds,
-                          gather, st);
+        launch_token_copy(ho.arg(), static_cast<int>(jobs.size()), static_cast<int>(max_parts), part_bytes,
+                          vw, lds, gather, st);
     });
 }
 

@@ -107,9 +107,10 @@ __device__ __forceinline__ void block_unit(const FastDiv& njobs, int& job, int& 
 
 template <int VW, bool GATHER, bool JOB_MINOR>
 __global__ __launch_bounds__(kThreads) void copy_pages_kernel(DescArg d, int job0, FastDiv njobs,
-                                                              int log2_parts) {
+                                                              int log2_parts, XcdRuns xr) {
     int jb, unit;
     block_unit<JOB_MINOR>(njobs, jb, unit);
+    if (!JOB_MINOR) unit = xr.map(unit);
     const CopyJob j = desc_load(desc_at<CopyJob>(d, 0) + job0 + jb);
     int p, s;
     uint8_t *cache, *stage;
@@ -397,22 +398,23 @@ void launch_copy_pages(const DescArg& d, int n_jobs, int max_tiles, int64_t max_
             const int nj = std::min(slice, n_jobs - j0);
             const FastDiv fd(static_cast<uint32_t>(nj));
             const dim3 grid(static_cast<unsigned>(units * nj));
-            if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, false, true>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
-            else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, false, true>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
-            else DARIC_LAUNCH((copy_pages_kernel<1, false, true>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
+            if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, false, true>), grid, kThreads, 0, stream, d, j0, fd, log2_parts, XcdRuns());
+            else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, false, true>), grid, kThreads, 0, stream, d, j0, fd, log2_parts, XcdRuns());
+            else DARIC_LAUNCH((copy_pages_kernel<1, false, true>), grid, kThreads, 0, stream, d, j0, fd, log2_parts, XcdRuns());
             check_launch("scatter_pages");
         }
         return;
     }
     // gather: tile-major within a job
     const FastDiv fd(1);
+    const int64_t gx = static_cast<int64_t>(max_tiles) << log2_parts;
+    const XcdRuns xr(gx, max_span >> log2_parts);
     for (int j0 = 0; j0 < n_jobs; j0 += kMaxY) {
         const int nj = std::min(kMaxY, n_jobs - j0);
-        const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(max_tiles) << log2_parts),
-                        static_cast<unsigned>(nj));
-        if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, true, false>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
-        else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, true, false>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
-        else DARIC_LAUNCH((copy_pages_kernel<1, true, false>), grid, kThreads, 0, stream, d, j0, fd, log2_parts);
+        const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(nj));
+        if (vw == 16) DARIC_LAUNCH((copy_pages_kernel<16, true, false>), grid, kThreads, 0, stream, d, j0, fd, log2_parts, xr);
+        else if (vw == 4) DARIC_LAUNCH((copy_pages_kernel<4, true, false>), grid, kThreads, 0, stream, d, j0, fd, log2_parts, xr);
+        else DARIC_LAUNCH((copy_pages_kernel<1, true, false>), grid, kThreads, 0, stream, d, j0, fd, log2_parts, xr);
         check_launch("gather_pages");
     }
 }

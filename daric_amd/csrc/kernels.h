@@ -34,6 +34,37 @@ struct RowGeomDiv {
     FastDiv ipr, tok_div, ps;
 };
 
+// XCD-aware unit order for grids whose consecutive units write consecutive
+// bytes (the gathers: staging is the contiguous side). Workgroups are
+// dispatched to the 8 XCDs round-robin, so with a grid row length divisible
+// by 8, unit u runs on XCD u % 8 and neighbouring parts of the staging side
+// would be written from different XCDs. map() permutes [0, full) so that XCD
+// x's i-th unit becomes unit (i / run * 8 + x) * run + i % run: each XCD
+// writes runs of `run` consecutive units. Runs of ~256 KiB measured fastest
+// on MI355X (gathers 1-3% faster than the plain order); runs of 32-64 KiB
+// were slower than the plain order. Units past `full` keep their place.
+struct XcdRuns {
+    static constexpr int kXcds = 8;
+    static constexpr int64_t kRunBytes = 256 * 1024;
+    int32_t log2_run = 0;   // 0: identity
+    int32_t full = 0;
+    XcdRuns() = default;
+    XcdRuns(int64_t grid_x, int64_t unit_bytes) {
+        if (grid_x % kXcds != 0 || unit_bytes <= 0) return;
+        while (log2_run < 10 && (unit_bytes << (log2_run + 1)) <= kRunBytes) ++log2_run;
+        const int64_t group = static_cast<int64_t>(kXcds) << log2_run;
+        full = static_cast<int32_t>(grid_x / group * group);
+    }
+#ifdef __HIPCC__
+    __host__ __device__
+#endif
+    inline int map(int u) const {
+        if (log2_run == 0 || u >= full) return u;
+        const int i = u >> 3, x = u & 7;
+        return ((((i >> log2_run) << 3) + x) << log2_run) + (i & ((1 << log2_run) - 1));
+    }
+};
+
 // One token-major copy job: the pages idx[0 .. n_sel) of one layer to or from
 // staging laid out as [n_kv][n_sel * PS][H][row_bytes] (K rows, then V rows).
 // A workgroup moves one part: part_tokens consecutive tokens (all heads) of
@@ -59,8 +90,9 @@ static_assert(sizeof(TokenJob) == 112, "TokenJob layout");
 
 // Token-major gather (staging <- cache) or scatter; lds selects the
 // LDS-staged transpose for head-major pages ([H, PS, D] dense); vw is 16 or 1.
-void launch_token_copy(const DescArg& d, int n_jobs, int max_parts, int vw, bool lds,
-                       bool gather, hipStream_t stream);
+// part_bytes: the largest part's staging bytes (sets the XCD run length).
+void launch_token_copy(const DescArg& d, int n_jobs, int max_parts, int64_t part_bytes, int vw,
+                       bool lds, bool gather, hipStream_t stream);
 
 // Plain page copies of the n_jobs CopyJobs in `d`. vw is the access width in
 // bytes (16, 4 or 1); max_span

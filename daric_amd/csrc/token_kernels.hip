@@ -100,10 +100,11 @@ __device__ __forceinline__ void block_part(FastDiv njobs, int& job, int& q) {
 }
 
 template <int VW, bool GATHER, bool JOB_MINOR>
-__global__ __launch_bounds__(kThreads) void token_rows_kernel(DescArg d, int job0, FastDiv njobs) {
+__global__ __launch_bounds__(kThreads) void token_rows_kernel(DescArg d, int job0, FastDiv njobs, XcdRuns xr) {
     using T = typename Unit<VW>::T;
     int jb, q;
     block_part<JOB_MINOR>(njobs, jb, q);
+    if (!JOB_MINOR) q = xr.map(q);
     const TokenJob j = desc_load(desc_at<TokenJob>(d, 0) + job0 + jb);
     uint8_t *cache, *stage;
     int n_tok;
@@ -139,10 +140,11 @@ __global__ __launch_bounds__(kThreads) void token_rows_kernel(DescArg d, int job
 // Head-major pages: the cache side of a part is H runs of n_tok rows, each
 // run contiguous (token stride == row bytes, head stride == PS * row bytes).
 template <bool GATHER, bool JOB_MINOR>
-__global__ __launch_bounds__(kThreads) void token_lds_kernel(DescArg d, int job0, FastDiv njobs) {
+__global__ __launch_bounds__(kThreads) void token_lds_kernel(DescArg d, int job0, FastDiv njobs, XcdRuns xr) {
     __shared__ u32x4 sm[kLdsUnits];
     int jb, q;
     block_part<JOB_MINOR>(njobs, jb, q);
+    if (!JOB_MINOR) q = xr.map(q);
     const TokenJob j = desc_load(desc_at<TokenJob>(d, 0) + job0 + jb);
     uint8_t *cache, *stage;
     int n_tok;
@@ -214,19 +216,19 @@ __global__ __launch_bounds__(kThreads) void token_lds_kernel(DescArg d, int job0
 
 }  // namespace
 
-void launch_token_copy(const DescArg& d, int n_jobs, int max_parts, int vw, bool lds,
-                       bool gather, hipStream_t stream) {
-#define DARIC_TOK(JM, FD)                                                                              \
+void launch_token_copy(const DescArg& d, int n_jobs, int max_parts, int64_t part_bytes, int vw,
+                       bool lds, bool gather, hipStream_t stream) {
+#define DARIC_TOK(JM, FD, XR)                                                                            \
     do {                                                                                               \
         if (lds) {                                                                                     \
-            if (gather) DARIC_LAUNCH((token_lds_kernel<true, JM>), grid, kThreads, 0, stream, d, j0, FD);  \
-            else DARIC_LAUNCH((token_lds_kernel<false, JM>), grid, kThreads, 0, stream, d, j0, FD);        \
+            if (gather) DARIC_LAUNCH((token_lds_kernel<true, JM>), grid, kThreads, 0, stream, d, j0, FD, XR);  \
+            else DARIC_LAUNCH((token_lds_kernel<false, JM>), grid, kThreads, 0, stream, d, j0, FD, XR);        \
         } else if (vw == 16) {                                                                         \
-            if (gather) DARIC_LAUNCH((token_rows_kernel<16, true, JM>), grid, kThreads, 0, stream, d, j0, FD); \
-            else DARIC_LAUNCH((token_rows_kernel<16, false, JM>), grid, kThreads, 0, stream, d, j0, FD);   \
+            if (gather) DARIC_LAUNCH((token_rows_kernel<16, true, JM>), grid, kThreads, 0, stream, d, j0, FD, XR); \
+            else DARIC_LAUNCH((token_rows_kernel<16, false, JM>), grid, kThreads, 0, stream, d, j0, FD, XR);   \
         } else {                                                                                       \
-            if (gather) DARIC_LAUNCH((token_rows_kernel<1, true, JM>), grid, kThreads, 0, stream, d, j0, FD); \
-            else DARIC_LAUNCH((token_rows_kernel<1, false, JM>), grid, kThreads, 0, stream, d, j0, FD);    \
+            if (gather) DARIC_LAUNCH((token_rows_kernel<1, true, JM>), grid, kThreads, 0, stream, d, j0, FD, XR); \
+            else DARIC_LAUNCH((token_rows_kernel<1, false, JM>), grid, kThreads, 0, stream, d, j0, FD, XR);    \
         }                                                                                              \
         check_launch(gather ? "gather_tokens" : "scatter_tokens");                                    \
     } while (0)
@@ -237,15 +239,16 @@ void launch_token_copy(const DescArg& d, int n_jobs, int max_parts, int vw, bool
             const int nj = std::min(slice, n_jobs - j0);
             const FastDiv fd(static_cast<uint32_t>(nj));
             const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(max_parts) * nj));
-            DARIC_TOK(true, fd);
+            DARIC_TOK(true, fd, XcdRuns());
         }
         return;
     }
+    const XcdRuns xr(max_parts, part_bytes);
     for (int j0 = 0; j0 < n_jobs; j0 += kMaxY) {
         const int nj = std::min(kMaxY, n_jobs - j0);
         const dim3 grid(static_cast<unsigned>(max_parts), static_cast<unsigned>(nj));
         const FastDiv fd(1);
-        DARIC_TOK(false, fd);
+        DARIC_TOK(false, fd, xr);
     }
 #undef DARIC_TOK
 }
