@@ -863,6 +863,23 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
         // about 1024 items (vector path) or 2048 pairs (element path) per tile
         const int64_t tile_items = vec ? 1024 : 2048;
         g.tile_tokens = static_cast<int32_t>(std::max<int64_t>(1, tile_items / std::max<int64_t>(per_tok, 1)));
+        // Page tiles (rerotate_lane_kernel) when a page's K rows are dense
+        // rows of a power-of-two number (<= 64) of 16-byte units.
+        int path = vec ? kRotVec : kRotElem;
+        if (vec) {
+            const int64_t W = L.row_width;
+            const int64_t upr = W * e / 16;
+            int64_t tok_div = 0;
+            if (L.H == 1 && L.ss == W) tok_div = 1;
+            else if (L.H > 1 && L.ss == L.H * W && L.sh == W) tok_div = L.H;     // [PS, H, W] rows
+            else if (L.H > 1 && L.sh == L.PS * W && L.ss == W) tok_div = 1;      // [H, PS, W] rows
+            if (tok_div > 0 && (W * e) % 16 == 0 && upr > 0 && upr <= 64 && (upr & (upr - 1)) == 0 &&
+                L.PS * L.H * upr <= kIntMax) {
+                path = kRotLane;
+                g.upr = static_cast<int32_t>(upr);
+                g.tok_div = static_cast<int32_t>(tok_div);
+            }
+        }
 
         std::vector<RopeSeg> segs;
         int64_t tiles = 0;
@@ -882,7 +899,10 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
             rs.n_tokens = static_cast<int32_t>(s.n_tokens);
             rs.delta = static_cast<float>(s.delta);
             rs.tile_begin = static_cast<int32_t>(tiles);
-            tiles += (s.n_tokens + g.tile_tokens - 1) / g.tile_tokens;
+            if (path == kRotLane)
+                tiles += last_block - s.tok_start / L.PS + 1;   // the pages the segment touches
+            else
+                tiles += (s.n_tokens + g.tile_tokens - 1) / g.tile_tokens;
             segs.push_back(rs);
         }
         if (segs.empty()) return;
@@ -899,7 +919,7 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
         launch_rerotate_inplace(ho.arg(), static_cast<int>(seg_bytes), static_cast<int>(n_layers), g,
                                 static_cast<int>(segs.size()), static_cast<int>(tiles),
                                 static_cast<const int32_t*>(block_table->data), rope->inv_freq,
-                                kind, neox, vec, st);
+                                kind, neox, path, st);
     });
 }
 

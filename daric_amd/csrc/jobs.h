@@ -97,8 +97,10 @@ struct InplaceGeom {
     int32_t H;
     int32_t R;
     int32_t num_blocks;
-    int32_t n_rot;     // rotated items per head row
+    int32_t n_rot;     // rotated items per head row (lane path: rotated units per pair half)
     int32_t tile_tokens;
+    int32_t upr;       // lane path: 16-byte units per K row (a power of two dividing 64)
+    int32_t tok_div;   // lane path: rows per token step (H: token-major rows, 1: head-major)
 };
 
 struct RopeSeg {

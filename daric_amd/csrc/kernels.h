@@ -107,12 +107,15 @@ void launch_scatter_rotate(const DescArg& d, int n_jobs, int max_tiles,
                            hipStream_t stream);
 
 // In-place K re-rotation over segments of tokens. `d` holds the n_segs
-// RopeSegs, then (at byte layer_off) the n_layers K base pointers; `vec`
-// selects 16-byte (true) or per-element (false) access. fp8 codes are
-// rotated as stored (a per-head scale cancels in a linear rotation).
+// RopeSegs, then (at byte layer_off) the n_layers K base pointers. `path`:
+// kRotElem (per-element access), kRotVec (16-byte items, tiles of
+// g.tile_tokens tokens) or kRotLane (one tile per page of dense K rows, see
+// rerotate_lane_kernel). fp8 codes are rotated as stored (a per-head scale
+// cancels in a linear rotation).
+enum RotPath { kRotElem = 0, kRotVec = 1, kRotLane = 2 };
 void launch_rerotate_inplace(const DescArg& d, int layer_off, int n_layers, const InplaceGeom& g,
                              int n_segs, int n_tiles, const int32_t* block_table,
-                             const float* inv_freq, int kind, bool neox, bool vec, hipStream_t stream);
+                             const float* inv_freq, int kind, bool neox, int path, hipStream_t stream);
 
 // Selection kernels. deviation_tile_tokens: tokens per deviation workgroup
 // (the tiling launch_deviation expects in SelChunk::tile_begin).

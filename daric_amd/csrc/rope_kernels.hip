@@ -135,6 +135,128 @@ __global__ __launch_bounds__(kThreads) void rerotate_vec_kernel(
     }
 }
 
+// Page-tile variant for K rows that are dense in the page (token-major
+// [PS, H, W] or head-major [H, PS, W] rows, W a 16-byte multiple). A
+// workgroup takes the segment's tokens in one page of one layer; the
+// segment's tiles are its pages (the first and last may be partial). Unit
+// i of the page's K rows goes to lane i % 256, as in a plain copy, so every
+// lane keeps one position k = i % upr within its rows: its cos/sin values
+// stay in registers for the whole page, and the NeoX partner unit (k +/- nr)
+// of the same row sits in the same wavefront, fetched with a lane exchange.
+// Only units of the rotated part and of the segment's tokens are read and
+// written. Loads are nontemporal and stores plain: in place, nontemporal
+// stores of the lines just read ran 12% slower on MI355X. On the config-2
+// in-place call (32 layers x 7168 tokens) this kernel ran 3-4% faster than
+// the item kernel; 2, 4 or 8 units in flight per lane measured the same.
+template <typename T>
+__device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
+
+constexpr int kLaneUnroll = 2;
+
+
+template <int KIND, bool NEOX>
+__global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
+    DescArg d, int layer_off, int layer0, InplaceGeom g, int n_segs,
+    const int32_t* __restrict__ bt, const float* __restrict__ inv_freq, FastDiv d_tok, FastDiv d_ps) {
+    using E = Elem<KIND>;
+    constexpr int VE = E::VE;
+    constexpr int EPW = E::EPW;
+    constexpr int ES = KIND == kE4M3 ? 1 : 2;
+    constexpr int NC = NEOX ? VE : VE / 2;   // cos/sin values per lane
+    __shared__ float s_cos[kMaxHalfRot];
+    __shared__ float s_sin[kMaxHalfRot];
+
+    const DescPtr<RopeSeg> segs = desc_at<RopeSeg>(d, 0);
+    const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off) + layer0;
+    const int tile = static_cast<int>(blockIdx.x);
+    const RopeSeg sg = desc_load(segs + find_segment(segs, n_segs, tile));
+    if (sg.delta == 0.0f) return;
+    const int page = sg.tok_start / g.PS + (tile - sg.tile_begin);
+    const int page_tok0 = page * g.PS;
+    const int lo = max(sg.tok_start - page_tok0, 0);
+    const int hi = min(sg.tok_start + sg.n_tokens - page_tok0, g.PS);
+    if (hi <= lo) return;
+    const int blk = bt[sg.bt_offset + page];
+    if (blk < 0 || blk >= g.num_blocks) return;
+    u32x4* __restrict__ pg = reinterpret_cast<u32x4*>(layers[blockIdx.y] + static_cast<int64_t>(blk) * g.sb * ES);
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63;
+    const int log2_upr = __builtin_ctz(static_cast<unsigned>(g.upr));
+    const int k = tid & (g.upr - 1);
+    const int nr = g.n_rot;
+    const bool rot_lane = NEOX ? k < 2 * nr : k < nr;
+    const bool first = k < nr;
+    const int src_lane = (NEOX && rot_lane) ? (first ? lane + nr : lane - nr) : lane;
+    const int pi0 = NEOX ? (first ? k : k - nr) * VE : k * (VE / 2);
+    const int n_units = g.PS * g.H * g.upr;
+    const int half = g.R / 2;
+
+    float cs[NC], ss[NC];
+    for (int base = 0; base < n_units; base += kThreads * kLaneUnroll) {
+        u32x4 v[kLaneUnroll];
+        bool act[kLaneUnroll];
+#pragma unroll
+        for (int u = 0; u < kLaneUnroll; ++u) {
+            const int i = base + u * kThreads + tid;
+            const uint32_t r = static_cast<uint32_t>(i >> log2_upr);
+            const uint32_t q = d_tok.div(r);
+            const int token = static_cast<int>(q - d_ps.div(q) * static_cast<uint32_t>(g.PS));
+            act[u] = rot_lane && i < n_units && token >= lo && token < hi;
+            v[u] = u32x4{0u, 0u, 0u, 0u};
+            if (act[u]) v[u] = ld_nt(pg + i);
+        }
+        if (base == 0) {
+            for (int i = tid; i < half; i += kThreads) {
+                float sn, c;
+                sincosf(sg.delta * inv_freq[i], &sn, &c);
+                s_cos[i] = c;
+                s_sin[i] = sn;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < NC; ++e) {
+                const int pi = rot_lane ? pi0 + e : 0;
+                cs[e] = s_cos[pi];
+                ss[e] = (NEOX && first) ? -s_sin[pi] : s_sin[pi];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kLaneUnroll; ++u) {
+            u32x4 pv = v[u];
+            if (NEOX) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    pv[w] = static_cast<uint32_t>(__shfl(static_cast<int>(v[u][w]), src_lane, 64));
+            }
+            if (!act[u]) continue;
+            u32x4 out;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                float x[EPW];
+                E::unpack_word(v[u][w], x);
+                if (NEOX) {
+                    float y[EPW];
+                    E::unpack_word(pv[w], y);
+#pragma unroll
+                    for (int e = 0; e < EPW; ++e)
+                        x[e] = x[e] * cs[w * EPW + e] + y[e] * ss[w * EPW + e];
+                } else {
+#pragma unroll
+                    for (int m = 0; m < EPW / 2; ++m) {
+                        const int pi = w * (EPW / 2) + m;
+                        const float x1 = x[2 * m], x2 = x[2 * m + 1];
+                        x[2 * m] = x1 * cs[pi] - x2 * ss[pi];
+                        x[2 * m + 1] = x2 * cs[pi] + x1 * ss[pi];
+                    }
+                }
+                out[w] = E::pack_word(x);
+            }
+            pg[base + u * kThreads + tid] = out;
+        }
+    }
+}
+
 // Per-element variant for layouts whose rows or pair halves are not 16-byte
 // aligned. One item = one rotation pair; fp8 codes are rotated as stored, as
 // in the vector kernel.
@@ -194,16 +316,21 @@ __global__ __launch_bounds__(kThreads) void rerotate_elem_kernel(
 
 void launch_rerotate_inplace(const DescArg& d, int layer_off, int n_layers, const InplaceGeom& g,
                              int n_segs, int n_tiles, const int32_t* block_table,
-                             const float* inv_freq, int kind, bool neox, bool vec, hipStream_t stream) {
+                             const float* inv_freq, int kind, bool neox, int path, hipStream_t stream) {
     constexpr int kMaxY = 65535;
     const FastDiv d_tok(static_cast<uint32_t>(g.H * g.n_rot)), d_rot(static_cast<uint32_t>(g.n_rot)),
-        d_ps(static_cast<uint32_t>(g.PS));
+        d_ps(static_cast<uint32_t>(g.PS)), d_ltok(static_cast<uint32_t>(g.tok_div > 0 ? g.tok_div : 1));
     for (int l0 = 0; l0 < n_layers; l0 += kMaxY) {
         const int nl = n_layers - l0 < kMaxY ? n_layers - l0 : kMaxY;
         const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(nl));
 #define DARIC_RV(K, N) DARIC_LAUNCH((rerotate_vec_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq, d_tok, d_rot, d_ps)
 #define DARIC_RE(K, N) DARIC_LAUNCH((rerotate_elem_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq)
-        if (vec) {
+#define DARIC_RL(K, N) DARIC_LAUNCH((rerotate_lane_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq, d_ltok, d_ps)
+        if (path == kRotLane) {
+            if (kind == kBF16) { if (neox) DARIC_RL(kBF16, true); else DARIC_RL(kBF16, false); }
+            else if (kind == kF16) { if (neox) DARIC_RL(kF16, true); else DARIC_RL(kF16, false); }
+            else { if (neox) DARIC_RL(kE4M3, true); else DARIC_RL(kE4M3, false); }
+        } else if (path == kRotVec) {
             if (kind == kBF16) { if (neox) DARIC_RV(kBF16, true); else DARIC_RV(kBF16, false); }
             else if (kind == kF16) { if (neox) DARIC_RV(kF16, true); else DARIC_RV(kF16, false); }
             else { if (neox) DARIC_RV(kE4M3, true); else DARIC_RV(kE4M3, false); }
@@ -214,6 +341,7 @@ void launch_rerotate_inplace(const DescArg& d, int layer_off, int n_layers, cons
         }
 #undef DARIC_RV
 #undef DARIC_RE
+#undef DARIC_RL
         check_launch("rerotate_pages");
     }
 }

@@ -26,6 +26,8 @@ def make_layer(layout: str, nb: int, ps: int, h: int, d: int, dtype, gen, kind="
         phys, perm, pf = (nb, h, ps, 2 * d), None, True
     elif layout == "mla":        # [NB, PS, hidden]
         phys, perm, pf = (nb, ps, h * d), None, True
+    elif layout == "nhd_pad":    # [2, NB, PS, H, D] with 16 padding elements after each head row
+        phys, perm, pf = (2, nb, ps, h, d + 16), None, False
     else:
         raise ValueError(layout)
     n = int(np.prod(phys))
@@ -39,6 +41,8 @@ def make_layer(layout: str, nb: int, ps: int, h: int, d: int, dtype, gen, kind="
         t = torch.randn(n, generator=gen).to(dtype).view(phys)
     if perm is not None:
         t = t.permute(*perm)
+    if layout == "nhd_pad":
+        t = t[..., :d]
     return t, pf
 
 

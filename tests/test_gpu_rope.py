@@ -174,6 +174,20 @@ def test_inplace_layouts(dev, layout, dtype):
     inplace_case(dev, layout, dtype, True, 64, d=64 if dtype != torch.uint8 else 128)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.uint8])
+@pytest.mark.parametrize("neox", [True, False])
+def test_inplace_item_path_padded_rows(dev, dtype, neox):
+    # head rows followed by padding are not dense in the page: the 16-byte
+    # item kernel runs instead of the page-tile kernel
+    inplace_case(dev, "nhd_pad", dtype, neox, 64, d=64 if dtype != torch.uint8 else 128, seed=8)
+
+
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+def test_inplace_large_pages(dev, layout):
+    # 64-token pages of 8 heads x 128: 8192 units per page, several rounds per lane
+    inplace_case(dev, layout, torch.bfloat16, True, 128, nb=24, ps=64, h=8, d=128, L=2, seed=9)
+
+
 @pytest.mark.parametrize("neox", [True, False])
 @pytest.mark.parametrize("rotary_dim", [64, 24, 10])
 def test_inplace_pairing_and_element_path(dev, neox, rotary_dim):
