@@ -104,3 +104,66 @@ def test_gather_replays_match_eager_and_large_calls_refuse_capture(dev):
     for i in range(40):
         src = layers[i % 3][:, 1 + i // 3].contiguous().view(torch.uint8).reshape(2, span)
         assert torch.equal(got[i], src), i
+
+
+def test_fused_and_selection_replays_match_eager(dev):
+    # a two-job fused scatter + re-rotation, then deviation -> top-k -> merge
+    # over two chunks: every call small enough to carry its descriptors by value
+    g = torch.Generator().manual_seed(2)
+    L, NB, PS, H, D = 2, 32, 16, 8, 128
+    base = [torch.randn(2, NB, PS, H, D, generator=g).to(torch.bfloat16) for _ in range(L)]
+    span = PS * H * D * 2
+    per = 2 * 3 * span
+    store_cpu = torch.randn(L * per // 2, generator=g).to(torch.bfloat16).view(torch.uint8)
+    T = 64
+    k_new = torch.randn(L, T, H, D, generator=g).to(torch.bfloat16).to(dev)
+    v_new = torch.randn(L, T, H, D, generator=g).to(torch.bfloat16).to(dev)
+    bt = torch.tensor([4, 9, 2, 17], dtype=torch.int32, device=dev)
+    chunks = [(0, 0, 32, 5), (2, 32, 32, 7)]
+    inv = torch.from_numpy(orope.default_inv_freq(D, 500000.0)).to(dev)
+    idx = torch.tensor([3, 11, 20, 5, 6, 30], dtype=torch.int32, device=dev)
+    names = ["a", "b"]
+
+    def make():
+        layers = [t.to(dev) for t in base]
+        cp = cache_ops.CacheCopier()
+        for n, t in zip(names, layers):
+            cp.register_layer(n, t, False)
+        store = store_cpu.to(dev)
+        cp.register_store(store)
+        keys = torch.zeros(L, T, dtype=torch.float32, device=dev)
+        sel = torch.zeros(L, 2, 7, dtype=torch.int32, device=dev)
+        return dict(layers=layers, cp=cp, store=store, keys=keys, sel=sel)
+
+    def run(s):
+        s["cp"].scatter_pages_rerotate(names, [0, per], [per, per], idx, [0, 3, 6], [100, -37], [48, 40],
+                                       inv, D, True)
+        cache_ops.kv_deviation(s["layers"], False, bt, k_new, chunks, keys=s["keys"])
+        cache_ops.topk_per_chunk(s["keys"], chunks, kmax=7, out=s["sel"])
+        cache_ops.merge_rows(s["layers"], False, bt, k_new, v_new, chunks, s["sel"])
+
+    eager, cap = make(), make()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):       # warm-up outside the capture
+        run(make())
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(cap)
+    torch.cuda.synchronize()
+    for t, b in zip(cap["layers"], base):      # capturing ran nothing
+        assert torch.equal(t.cpu().view(torch.int16), b.view(torch.int16))
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        run(eager)
+        torch.cuda.synchronize()
+        for li in range(L):
+            assert torch.equal(cap["layers"][li].view(torch.int16), eager["layers"][li].view(torch.int16)), \
+                f"replay {rep} layer {li}"
+        assert torch.equal(cap["keys"], eager["keys"]), f"replay {rep} keys"
+        assert torch.equal(cap["sel"], eager["sel"]), f"replay {rep} sel"
+        _ = float(torch.randn(4096, device=dev).abs().sum())
+        torch.cuda.synchronize()
