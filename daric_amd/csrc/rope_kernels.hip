@@ -5,9 +5,12 @@
 // cos/sin table read from HBM. Here a workgroup takes a tile of tokens of one
 // segment (a run of tokens that all move by the same delta), computes the
 // segment's rotary_dim/2 cos/sin values once in fp32 into LDS, and streams
-// the tile's K head rows with 16-byte accesses (per-element accesses when the
-// layout is not 16-byte aligned). Only the rotated [0, R) part of each head
-// row is read and written; V and the rotary tail are never touched.
+// the tile's K head rows with 16-byte accesses. A tile is the segment's
+// tokens in one page when the page's K rows are dense (rerotate_lane_kernel),
+// else a run of about 1024 16-byte items (rerotate_vec_kernel), or of pairs
+// with per-element accesses when the layout is not 16-byte aligned
+// (rerotate_elem_kernel). Only the rotated [0, R) part of each head row is
+// read and written; V and the rotary tail are never touched.
 #include <hip/hip_runtime.h>
 
 #include "elem.h"
