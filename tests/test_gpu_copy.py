@@ -99,6 +99,37 @@ def test_large_pages_multi_round(dev):
     assert same_bytes(sd, sc)
 
 
+@pytest.mark.parametrize("n_sel", [32, 33, 35, 40])
+def test_gather_xcd_runs_with_tail(dev, n_sel):
+    # 32 KiB page spans in 4 parts of 8 KiB: 8 * n_sel units in the largest
+    # job. Units are dealt to the XCDs in runs of 32 up to the largest multiple
+    # of 256; the tail (0, 8, 24 or 64 units) keeps its place. The second job is
+    # shorter, a null page and an out-of-range page sit in both regions.
+    g = torch.Generator().manual_seed(21 + n_sel)
+    nb = 64
+    t, pf = make_layer("nhd", nb, 16, 8, 128, torch.bfloat16, g, kind="bytes")
+    u, _ = make_layer("nhd", nb, 16, 8, 128, torch.bfloat16, g, kind="bytes")
+    span = 16 * 8 * 128 * 2
+    sel = [int(x) for x in np.random.default_rng(n_sel).permutation(np.arange(1, nb))[:n_sel]]
+    sel[2], sel[-3] = 0, nb + 7
+    sel2 = sel[: n_sel - 9]
+    oc, gc = OracleCopier(), cache_ops.CacheCopier()
+    for name, x in (("x", t), ("y", u)):
+        oc.register_layer(name, x, pf)
+        gc.register_layer(name, to_dev(x, dev), pf)
+    n1, n2 = 2 * len(sel) * span, 2 * len(sel2) * span
+    store = torch.randint(0, 256, (n1 + n2,), dtype=torch.uint8, generator=g)
+    oc.register_store(store.clone())
+    sd = store.to(dev)
+    gc.register_store(sd)
+    idx = torch.tensor(sel + sel2, dtype=torch.int32)
+    args = (["x", "y"], [0, n1], [n1, n2])
+    oc.gather_pages(*args, idx, [0, len(sel), len(sel) + len(sel2)])
+    gc.gather_pages(*args, idx.to(dev), [0, len(sel), len(sel) + len(sel2)])
+    torch.cuda.synchronize()
+    assert same_bytes(sd, oc.store)
+
+
 def test_errors_surface_as_runtime_error(dev):
     gc = cache_ops.CacheCopier()
     t = torch.zeros(2, 4, 16, 2, 8, dtype=torch.bfloat16, device=dev)

@@ -88,6 +88,17 @@ def test_token_copies_llama3_8b_hnd(dev, gather):
           sels=[list(range(1, 33)), [5, 0, 7, 39, 41]])
 
 
+@pytest.mark.parametrize("n_sel", [33, 35, 40])
+def test_token_gather_xcd_runs_with_tail(dev, n_sel):
+    # 8 KiB parts, 2 * n_sel * 4 per job: runs of 32 parts per XCD cover the
+    # largest multiple of 256 and the tail (8, 24 or 64 parts) keeps its place;
+    # a null page and an out-of-range page sit in both regions
+    sel = list(range(1, n_sel + 1))
+    sel[3], sel[-2] = 0, 99
+    _case(dev, ["hnd", "pf_hnd"], torch.bfloat16, nb=48, h=8, d=128, gather=True, seed=7 + n_sel,
+          sels=[sel, sel[: n_sel - 5]])
+
+
 def test_gather_tokens_canonical_rows_at_size(dev):
     """An HND cache gathered token-major equals torch's own permute of the
     selected pages (2 layers x 256 pages of [H=8, PS=16, D=128] bf16)."""
