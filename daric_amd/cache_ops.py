@@ -35,11 +35,19 @@ __all__ = [
 ]
 
 
+# The current stream's raw handle without building a torch.cuda.Stream object
+# (0.1 us against 2 us per call on MI355X); the public call is the fallback.
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _resolve_stream(stream: int, device: Optional[torch.device]) -> int:
     if stream:
         return int(stream)
     if device is None or device.type != "cuda":
         return 0
+    if _RAW_STREAM is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return int(_RAW_STREAM(idx))
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -164,6 +164,16 @@ def test_explicit_stream_and_default_stream(dev):
     gc.gather_pages(["a"], [0], [2048], idx, [0, 2])
     torch.cuda.synchronize()
     assert torch.equal(st, want)
+    # stream 0 is torch's current stream, also inside a stream context
+    assert cache_ops._resolve_stream(0, dev) == torch.cuda.current_stream().cuda_stream
+    s2 = torch.cuda.Stream()
+    with torch.cuda.stream(s2):
+        assert cache_ops._resolve_stream(0, dev) == s2.cuda_stream
+        assert cache_ops._resolve_stream(0, torch.device("cuda")) == s2.cuda_stream
+        st.zero_()
+        gc.gather_pages(["a"], [0], [2048], idx, [0, 2])
+    s2.synchronize()
+    assert torch.equal(st, want)
 
 
 def test_batched_memcpy_roundtrip(dev):
