@@ -16,6 +16,7 @@
 
 #include "../../include/daric_cache_ops.h"
 #include "jobs.h"
+#include "launch.h"
 
 namespace daric {
 
@@ -101,7 +102,11 @@ public:
     // descriptors over the host link. The caller must call release() with
     // the returned slot index after enqueueing every kernel that reads it.
     void* upload(const void* src, size_t bytes, hipStream_t stream, int* slot_out, bool direct = false);
-    void release(int slot, hipStream_t stream);
+    // The slot's reuse guard. If the caller's last kernel launch carried it
+    // (`bound`), it completes with that kernel; else release() records it on
+    // `stream`.
+    hipEvent_t slot_event(int slot) const { return slots_[slot].ev; }
+    void release(int slot, hipStream_t stream, bool bound = false);
 
 private:
     DescRing() = default;
@@ -115,13 +120,26 @@ private:
 
 // RAII helper: uploads a descriptor array (or, with `direct`, hands out its
 // pinned host copy) and releases its slot at scope exit.
+// While it lives, the slot's event is the calling thread's completion event
+// (see DARIC_LAUNCH), so the call's kernels carry it.
+void set_completion_event(hipEvent_t ev);
+hipEvent_t completion_bound();
+
 class DescUpload {
 public:
     DescUpload(int device, const void* src, size_t bytes, hipStream_t stream, bool direct = false)
         : ring_(DescRing::for_device(device)), stream_(stream) {
         ptr_ = ring_.upload(src, bytes, stream, &slot_, direct);
+        ev_ = ring_.slot_event(slot_);
+        prev_ = completion_event();
+        set_completion_event(ev_);
     }
-    ~DescUpload() { ring_.release(slot_, stream_); }
+    ~DescUpload() {
+        // bound: the last launch since the constructor carried this slot's event
+        const bool bound = completion_bound() == ev_;
+        set_completion_event(prev_);
+        ring_.release(slot_, stream_, bound);
+    }
     void* get() const { return ptr_; }
 
 private:
@@ -129,6 +147,8 @@ private:
     hipStream_t stream_;
     int slot_ = -1;
     void* ptr_ = nullptr;
+    hipEvent_t ev_ = nullptr;
+    hipEvent_t prev_ = nullptr;
 };
 
 // Hands a call's descriptor bytes to its kernels: inline in the kernel

@@ -158,16 +158,31 @@ void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* s
     return s.dev;
 }
 
-void DescRing::release(int slot, hipStream_t stream) {
+void DescRing::release(int slot, hipStream_t stream, bool bound) {
     if (slot < 0) return;
     std::lock_guard<std::mutex> lk(mu_);
     Slot& s = slots_[slot];
-    // The event marks the end of every kernel that reads the slot; if it
-    // cannot be recorded, wait for the stream instead so reuse stays safe.
-    if (hipEventRecord(s.ev, stream) == hipSuccess) s.pending = true;
+    // The event marks the end of every kernel that reads the slot: the last
+    // one carried it (kernels of one stream finish in order), or it is
+    // recorded here; if it cannot be, wait for the stream so reuse stays safe.
+    if (bound) s.pending = true;
+    else if (hipEventRecord(s.ev, stream) == hipSuccess) s.pending = true;
     else (void)hipStreamSynchronize(stream);
     s.in_use = false;
 }
+
+namespace {
+thread_local hipEvent_t t_completion = nullptr;
+thread_local hipEvent_t t_completion_bound = nullptr;
+}  // namespace
+
+void set_completion_event(hipEvent_t ev) {
+    t_completion = ev;
+    t_completion_bound = nullptr;
+}
+hipEvent_t completion_event() { return t_completion; }
+void note_completion_bound(hipEvent_t ev) { t_completion_bound = ev; }
+hipEvent_t completion_bound() { return t_completion_bound; }
 
 // ---------------------------------------------------------------- timing
 void timing_events(hipEvent_t* start, hipEvent_t* stop) {
