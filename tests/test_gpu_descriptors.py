@@ -93,3 +93,48 @@ def test_fused_with_grown_direct_slot(dev):
         # every layer's V half is a plain copy: bit-exact
         for li in range(N_LAYERS):
             assert same_bytes(dev_layers[li][1], layers[li][1]), f"seed {seed} layer {li}"
+
+
+def test_back_to_back_calls_reuse_slots_safely(dev):
+    # 40 fused calls with no synchronisation between them, each with 48 jobs
+    # (3840 bytes of descriptors: a ring slot, read directly by the kernels).
+    # The 16 slots are reused 2.5 times; every call writes its own pages with
+    # its own shifts, so a slot rewritten before its kernel finished would
+    # show up as a wrong rotation. Each slot's reuse waits for the event its
+    # call's kernel carries.
+    n_calls, n_jobs, nb, ps, h, d = 40, 48, 2048, 4, 1, 16
+    R = d
+    inv = orope.default_inv_freq(R, 10000.0)
+    g = torch.Generator().manual_seed(11)
+    layer = torch.randn(2, nb, ps, h, d, generator=g).to(torch.bfloat16)
+    span = ps * h * d * 2
+    pages = np.random.default_rng(11).permutation(np.arange(1, nb))[: n_calls * n_jobs].tolist()
+    store = torch.randn(n_calls * n_jobs * span, generator=g).to(torch.bfloat16).view(torch.uint8)
+    oc, gc = _oracle(), cache_ops.CacheCopier()
+    oc.register_layer("l", layer, False)
+    dl = layer.to(dev)
+    gc.register_layer("l", dl, False)
+    oc.register_store(store.clone())
+    gc.register_store(store.to(dev))
+    invd = torch.from_numpy(inv).to(dev)
+    calls = []
+    for c in range(n_calls):
+        jp = pages[c * n_jobs:(c + 1) * n_jobs]
+        offs = [(c * n_jobs + j) * 2 * span for j in range(n_jobs)]
+        deltas = [1 + 97 * c + j for j in range(n_jobs)]
+        calls.append((["l"] * n_jobs, offs, [2 * span] * n_jobs, torch.tensor(jp, dtype=torch.int32),
+                      list(range(n_jobs + 1)), deltas, [ps] * n_jobs))
+    idx_dev = [ci[3].to(dev) for ci in calls]
+    torch.cuda.synchronize()
+    # a bounded spin ahead of the calls keeps their kernels queued, so the
+    # 17th call must wait for the first call's kernel to release slot 0
+    torch.cuda._sleep(50_000_000)
+    for ci, idd in zip(calls, idx_dev):
+        gc.scatter_pages_rerotate(ci[0], ci[1], ci[2], idd, ci[4], ci[5], ci[6], invd, R, True)
+    for ci in calls:
+        oc.scatter_pages_rerotate(ci[0], ci[1], ci[2], ci[3], ci[4], ci[5], ci[6], inv, R, True)
+    torch.cuda.synchronize()
+    slots = [p * ps + j for p in pages for j in range(ps)]
+    mask, pn = rotation_region(layer, False, R, slots, True)
+    assert_rotation_parity(dl, layer, mask, pn)
+    assert same_bytes(dl[1], layer[1])
