@@ -11,12 +11,17 @@ position.
 
 Pipeline: the reference gathers a batch into one staging buffer, copies it to
 host, and only then gathers the next batch, with a full stream synchronisation
-per load chunk. Here staging is split into two halves: the copy kernels run on
-the compute stream and the host DMA on a copy stream, so batch b+1's
-gather (scatter) overlaps batch b's device-to-host (host-to-device) copy; events
-order each half's reuse. Both streams keep the default priority. Batching keeps
-the reference's limits: at most MAX_BATCH_SIZE metas and one staging half of
-bytes per batch on store; load chunks bounded by the staging half.
+per load chunk. Here each direction's staging is split into two halves: the
+copy kernels run on a kernel stream and the host DMA on a DMA stream, so batch
+b+1's gather (scatter) overlaps batch b's device-to-host (host-to-device)
+copy; events order each half's reuse. All streams keep the default priority.
+Batching keeps the reference's limits: at most MAX_BATCH_SIZE metas and one
+staging half of bytes per batch on store; load chunks bounded by the staging
+half.
+
+Store and load have separate staging buffers and streams, as the reference's
+staging and read_staging (gpu_kv_io.py:150-151), so one thread may store while
+another loads. Two stores, or two loads, must not run at once on one context.
 
 The host buffer must be page-locked memory (torch pin_memory or hipHostMalloc)
 so the DMA engines can reach it.
@@ -97,10 +102,23 @@ def build_copy_plan(layer_names, group_idxs, layer_bpbs, offsets, block_ids_list
     return np.asarray(flat, dtype=np.int32), job_off, ioff, job_names, job_sz
 
 
+class _Pipe:
+    """One direction's double-buffered staging: two halves of `half` bytes, a
+    stream for the copy kernels, a stream for the host DMA, and per half the
+    event after which it may be overwritten."""
+
+    def __init__(self, half: int, device: torch.device):
+        self.half = half
+        self.staging = torch.empty(2 * half, dtype=torch.uint8, device=device)
+        self.kernels = torch.cuda.Stream(device=device)
+        self.dma = torch.cuda.Stream(device=device)
+        self.half_free = [None, None]
+
+
 class KVIOContext:
-    """One GPU's store/load context: a write copier (gathers into staging) and
-    a read copier (scatters from staging), two staging halves, a compute
-    stream and a copy stream."""
+    """One GPU's store/load context: a write copier (gathers into the store
+    staging) and a read copier (scatters from the load staging), each direction
+    with two staging halves, a kernel stream and a DMA stream."""
 
     MAX_BATCH_SIZE = 4
 
@@ -122,17 +140,16 @@ class KVIOContext:
         self.half = int(staging_bytes) // 2 // 256 * 256
         if self.half <= 0:
             raise ValueError("staging_bytes too small")
-        self.staging = torch.empty(2 * self.half, dtype=torch.uint8, device=self.device)
-        self.compute = torch.cuda.Stream(device=self.device)
-        self.copy = torch.cuda.Stream(device=self.device)
+        self._store = _Pipe(self.half, self.device)
+        self._load = _Pipe(self.half, self.device)
         self.write_copier = cache_ops.CacheCopier()
         self.read_copier = cache_ops.CacheCopier()
         for name, pf in zip(self.layer_names, self.page_firsts):
             self.write_copier.register_layer(name, kv_caches[name], bool(pf))
             self.read_copier.register_layer(name, kv_caches[name], bool(pf))
-        self.write_copier.register_store(self.staging)
-        self.read_copier.register_store(self.staging)
-        self._half_free = [None, None]   # event after which a staging half may be overwritten
+        self.write_copier.register_store(self._store.staging)
+        self.read_copier.register_store(self._load.staging)
+        self.done = None   # after load(): event marking the end of its device work
 
     # ------------------------------------------------------------ helpers
     def cache_sizes(self, block_ids_list, layer_name=None) -> List[int]:
@@ -174,8 +191,9 @@ class KVIOContext:
         are in host memory."""
         offsets = [int(o) for o in offsets]
         sizes = self.cache_sizes(block_ids_list, layer_name)
+        pipe = self._store
         if wait_stream is not None:
-            self.compute.wait_stream(wait_stream)
+            pipe.kernels.wait_stream(wait_stream)
         per_meta = 1 if layer_name is not None else len(self.layer_names)
         b = 0
         for i, j in self._batches(sizes, self.half, self.MAX_BATCH_SIZE):
@@ -185,23 +203,23 @@ class KVIOContext:
                 self.layer_names, self.group_idxs, self.layer_bpbs, offsets[i:j],
                 block_ids_list[i:j], layer_name)
             stg = np.cumsum([0] + job_sz[:-1]).astype(np.int64) + base
-            if self._half_free[h] is not None:
-                self.compute.wait_event(self._half_free[h])
-            with torch.cuda.stream(self.compute):
+            if pipe.half_free[h] is not None:
+                pipe.kernels.wait_event(pipe.half_free[h])
+            with torch.cuda.stream(pipe.kernels):
                 idx = torch.from_numpy(flat).to(self.device, non_blocking=False)
             self.write_copier.gather_pages(names, stg.tolist(), job_sz, idx, ioff,
-                                           self.compute.cuda_stream)
-            done = torch.cuda.Event()
-            done.record(self.compute)
-            self.copy.wait_event(done)
+                                           pipe.kernels.cuda_stream)
+            gathered = torch.cuda.Event()
+            gathered.record(pipe.kernels)
+            pipe.dma.wait_event(gathered)
             meta_stg = [int(stg[k * per_meta]) for k in range(j - i)]
             cs, ch, cn = split_registration_copies(meta_stg, offsets[i:j], sizes[i:j])
-            cache_ops.batched_memcpy_d2h(self.staging, self.host, cs, ch, cn, self.copy.cuda_stream)
+            cache_ops.batched_memcpy_d2h(pipe.staging, self.host, cs, ch, cn, pipe.dma.cuda_stream)
             ev = torch.cuda.Event()
-            ev.record(self.copy)
-            self._half_free[h] = ev
+            ev.record(pipe.dma)
+            pipe.half_free[h] = ev
             b += 1
-        self.copy.synchronize()
+        pipe.dma.synchronize()
         self._write_positions([o + s for o, s in zip(offsets, sizes)], saved_positions)
 
     # ------------------------------------------------------------ load
@@ -214,12 +232,14 @@ class KVIOContext:
         saved position to new_positions[i] in the same pass
         (scatter_pages_rerotate); the saved positions are read from the headers
         first, which live in host memory. Device work is left queued on the
-        compute stream; the returned event marks its end."""
+        load's kernel stream; self.done, an event recorded after it, marks its
+        end."""
         offsets = [int(o) for o in offsets]
         sizes = self.cache_sizes(block_ids_list, layer_name)
         saved = self.read_positions([o + s for o, s in zip(offsets, sizes)])
+        pipe = self._load
         if wait_stream is not None:
-            self.copy.wait_stream(wait_stream)
+            pipe.dma.wait_stream(wait_stream)
         per_meta = 1 if layer_name is not None else len(self.layer_names)
         b = 0
         for i, j in self._batches(sizes, self.half, 1 << 30):
@@ -229,29 +249,29 @@ class KVIOContext:
                 self.layer_names, self.group_idxs, self.layer_bpbs, offsets[i:j],
                 block_ids_list[i:j], layer_name)
             stg = np.cumsum([0] + job_sz[:-1]).astype(np.int64) + base
-            if self._half_free[h] is not None:
-                self.copy.wait_event(self._half_free[h])
+            if pipe.half_free[h] is not None:
+                pipe.dma.wait_event(pipe.half_free[h])
             meta_stg = [int(stg[k * per_meta]) for k in range(j - i)]
             cs, ch, cn = split_registration_copies(meta_stg, offsets[i:j], sizes[i:j])
-            cache_ops.batched_memcpy_h2d(self.host, self.staging, ch, cs, cn, self.copy.cuda_stream)
+            cache_ops.batched_memcpy_h2d(self.host, pipe.staging, ch, cs, cn, pipe.dma.cuda_stream)
             arrived = torch.cuda.Event()
-            arrived.record(self.copy)
-            self.compute.wait_event(arrived)
-            with torch.cuda.stream(self.compute):
+            arrived.record(pipe.dma)
+            pipe.kernels.wait_event(arrived)
+            with torch.cuda.stream(pipe.kernels):
                 idx = torch.from_numpy(flat).to(self.device, non_blocking=False)
             if rerotate is None:
                 self.read_copier.scatter_pages(names, stg.tolist(), job_sz, idx, ioff,
-                                               self.compute.cuda_stream)
+                                               pipe.kernels.cuda_stream)
             else:
                 new_pos, ntok, inv, rdim, neox = rerotate
                 deltas = [int(new_pos[k]) - int(saved[k]) for k in range(i, j) for _ in range(per_meta)]
                 nt = [int(ntok[k]) for k in range(i, j) for _ in range(per_meta)]
                 self.read_copier.scatter_pages_rerotate(names, stg.tolist(), job_sz, idx, ioff, deltas,
-                                                        nt, inv, rdim, neox, self.compute.cuda_stream)
+                                                        nt, inv, rdim, neox, pipe.kernels.cuda_stream)
             ev = torch.cuda.Event()
-            ev.record(self.compute)
-            self._half_free[h] = ev
+            ev.record(pipe.kernels)
+            pipe.half_free[h] = ev
             b += 1
         self.done = torch.cuda.Event()
-        self.done.record(self.compute)
+        self.done.record(pipe.kernels)
         return saved

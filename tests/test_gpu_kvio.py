@@ -133,3 +133,50 @@ def test_load_rerotate_matches_oracle(dev):
     for n in names:
         mask, pn = rotation_region(fresh_cpu[n], pf, R, slots, True)
         assert_rotation_parity(fresh_dev[n], fresh_cpu[n], mask, pn)
+
+
+def test_store_and_load_from_two_threads(dev):
+    # One context, one thread storing records of some blocks while another loads
+    # earlier records into other blocks: store and load have their own staging
+    # halves and streams, as the reference's staging and read_staging
+    # (gpu_kv_io.py:150-151). Small staging halves make both pipelines run
+    # several batches at once.
+    import threading
+    names, cpu, pf, bpb, groups = setup(dev, nb=160)
+    rng = np.random.default_rng(4)
+    perm = rng.permutation(np.arange(1, 160)).tolist()
+    cut = lambda lo, n: [(perm[lo + 3 * k: lo + 3 * k + 3],) for k in range(n)]
+    src_y, blk_x, dst_l = cut(0, 12), cut(36, 12), cut(72, 12)     # disjoint block sets
+    host = torch.zeros(64 << 20, dtype=torch.uint8, pin_memory=True)
+    dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
+    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, dev_caches, host, staging_bytes=320 << 10)
+    rec = ctx.record_size(src_y[0])
+    offs_y = [8192 + k * (rec + 512) for k in range(12)]
+    offs_x = [(16 << 20) + k * (rec + 512) for k in range(12)]
+    saved_y, saved_x = list(range(100, 112)), list(range(200, 212))
+    ctx.store(offs_y, src_y, saved_y)
+    torch.cuda.synchronize()
+    shm = host.clone()
+    errors = []
+
+    def run(fn):
+        try:
+            for _ in range(3):
+                fn()
+        except Exception as e:      # surfaced below
+            errors.append(e)
+
+    got = {}
+    t1 = threading.Thread(target=run, args=(lambda: ctx.store(offs_x, blk_x, saved_x),))
+    t2 = threading.Thread(target=run, args=(lambda: got.__setitem__("pos", ctx.load(offs_y, dst_l)),))
+    t1.start(); t2.start(); t1.join(); t2.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    assert got["pos"] == saved_y
+    ocpu = {n: t.clone() for n, t in cpu.items()}
+    ok = okv.OracleKVIO(names, groups, bpb, [pf] * 3, ocpu, shm)
+    ok.store(offs_x, blk_x, saved_x)
+    ok.load(offs_y, dst_l)
+    assert torch.equal(host, shm), "stored records differ from the oracle's"
+    for n in names:
+        assert same_bytes(dev_caches[n], ocpu[n])
