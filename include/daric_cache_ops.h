@@ -20,6 +20,10 @@
  *    except where a function says so.
  *  - Host-side validation happens before any device work, so a failing call
  *    leaves device memory untouched.
+ *  - A call whose job descriptors fit in 2816 bytes passes them in the kernel
+ *    arguments and enqueues only kernels, so it may be recorded by a HIP
+ *    stream capture. A larger call stages them in a per-device ring of pinned
+ *    slots and returns DARIC_ERR_INVALID while `stream` is capturing.
  */
 #ifndef DARIC_CACHE_OPS_H
 #define DARIC_CACHE_OPS_H
