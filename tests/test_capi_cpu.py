@@ -294,3 +294,45 @@ def test_host_bf16_f16_conversion_matches_torch(hosttest):
 def test_host_fastdiv(hosttest, d):
     assert hosttest.daric_hosttest_fastdiv_errors(d, 0, 1 << 20) == 0
     assert hosttest.daric_hosttest_fastdiv_errors(d, (1 << 31) - (1 << 18), 1 << 31) == 0
+
+
+C_CONSUMER = r"""
+#include <stdio.h>
+#include <string.h>
+#include "daric_cache_ops.h"
+
+int main(void) {
+    daric_copier* c = NULL;
+    if (daric_abi_version() != DARIC_ABI_VERSION) { puts("abi"); return 1; }
+    if (daric_copier_create(&c) != DARIC_OK || c == NULL) { puts("create"); return 2; }
+    /* no store registered: the reference's first check (copier.cpp:46) */
+    int64_t off = 0, size = 16, ioff[2] = {0, 1};
+    const char* names[1] = {"model.layers.0.self_attn.attn"};
+    daric_tensor idx;
+    memset(&idx, 0, sizeof idx);
+    int st = daric_copier_gather_pages(c, names, 1, &off, 1, &size, 1, &idx, ioff, 2, 0);
+    if (st == DARIC_OK) { puts("gather accepted a call without a store"); return 3; }
+    printf("status %d: %s\n", st, daric_last_error());
+    if (daric_copier_destroy(c) != DARIC_OK) { puts("destroy"); return 4; }
+    return 0;
+}
+"""
+
+
+def test_c_consumer_compiles_and_links(lib, tmp_path):
+    # the header is plain C99 and the library links and runs from a C program
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    src = tmp_path / "consumer.c"
+    src.write_text(C_CONSUMER)
+    exe = tmp_path / "consumer"
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), str(src),
+                    "-o", str(exe), "-L", libdir, "-ldaric_cache_ops", f"-Wl,-rpath,{libdir}"],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "store buffer not registered" in out.stdout
