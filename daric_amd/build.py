@@ -26,7 +26,7 @@ SOURCES = ["capi.cpp", "runtime.cpp", "copy_kernels.hip", "rope_kernels.hip", "s
            "token_kernels.hip"]
 
 ARCH = "gfx950"
-COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
+COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wshadow", "-Wno-unused-result",
           f"-I{os.path.join(ROOT, 'include')}"]
 # Keep the compiler from emitting packed fp32 VALU ops (v_pk_*_f32).
 NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

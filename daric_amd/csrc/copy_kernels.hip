@@ -371,10 +371,10 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
                     E::unpack_word(pv[w], y);
                     if (CSL) {
                         // pairs pi0 + w*EPW .. +EPW-1: EPW/2 float4 reads
-                        const float4* q = s_cs + ((pi0 + w * EPW) >> 1);
+                        const float4* csq = s_cs + ((pi0 + w * EPW) >> 1);
 #pragma unroll
                         for (int h2 = 0; h2 < EPW / 2; ++h2) {
-                            const float4 t = q[h2];
+                            const float4 t = csq[h2];
                             const float s0 = first ? -t.y : t.y, s1 = first ? -t.w : t.w;
                             x[2 * h2] = x[2 * h2] * t.x + y[2 * h2] * s0;
                             x[2 * h2 + 1] = x[2 * h2 + 1] * t.z + y[2 * h2 + 1] * s1;
@@ -390,9 +390,9 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
                         const int pi = w * (EPW / 2) + m;
                         float c, sn;
                         if (CSL) {
-                            const float* q = reinterpret_cast<const float*>(s_cs) + 2 * (pi0 + pi);
-                            c = q[0];
-                            sn = q[1];
+                            const float* csq = reinterpret_cast<const float*>(s_cs) + 2 * (pi0 + pi);
+                            c = csq[0];
+                            sn = csq[1];
                         } else {
                             c = cs[pi];
                             sn = ss[pi];

@@ -145,8 +145,8 @@ __global__ __launch_bounds__(kThreads) void deviation_kernel(
             unpack8<CK>(rb[i], b, scale);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float d = a[e] - b[e];
-                const float sq = d * d;
+                const float df = a[e] - b[e];
+                const float sq = df * df;
                 acc[i] = acc[i] + sq;
             }
         }
