@@ -9,7 +9,8 @@ import pytest
 from daric_amd.policy import DARICPolicy, cluster_groups, recompute_counts
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-VECTORS = json.load(open(os.path.join(HERE, "golden", "policy_vectors.json")))
+with open(os.path.join(HERE, "golden", "policy_vectors.json")) as _f:
+    VECTORS = json.load(_f)
 
 
 def _policies():
