@@ -71,8 +71,9 @@ def fixed_order_sumsq(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     a = np.asarray(a, np.float32)
     b = np.asarray(b, np.float32)
     t, n = a.shape
-    d = (a - b).astype(np.float32)
-    sq = (d * d).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):   # inf - inf and overflow give NaN / inf, as on the GPU
+        d = (a - b).astype(np.float32)
+        sq = (d * d).astype(np.float32)
     n_vec = -(-n // VEC)
     rounds = -(-n_vec // LANES)
     padded = np.zeros((t, rounds * LANES * VEC), np.float32)
