@@ -180,3 +180,68 @@ def test_store_and_load_from_two_threads(dev):
     assert torch.equal(host, shm), "stored records differ from the oracle's"
     for n in names:
         assert same_bytes(dev_caches[n], ocpu[n])
+
+
+KV_FUZZ = None
+try:
+    from hypothesis import HealthCheck, given, settings
+    from hypothesis import strategies as st
+    KV_FUZZ = settings(max_examples=25, deadline=None, derandomize=True, database=None,
+                       suppress_health_check=[HealthCheck.too_slow, HealthCheck.function_scoped_fixture])
+except ImportError:      # hypothesis is part of the image; keep the module importable without it
+    pass
+
+
+if KV_FUZZ is not None:
+    @KV_FUZZ
+    @given(data=st.data())
+    def test_store_load_fuzz(dev, data):
+        # drawn layout, dtype, group count, meta count, blocks per meta (null
+        # ids included), layerwise or whole records and staging size; host
+        # records bit-exact after store, caches bit-exact after load
+        layout = data.draw(st.sampled_from(["nhd", "hnd", "pf", "pf_hnd", "packed", "mla"]), label="layout")
+        dtype = data.draw(st.sampled_from([torch.bfloat16, torch.float16, torch.uint8]), label="dtype")
+        two = data.draw(st.booleans(), label="two_groups") and layout != "mla"
+        n_layers = data.draw(st.integers(1, 4), label="layers")
+        n_meta = data.draw(st.integers(1, 9), label="metas")
+        seed = data.draw(st.integers(0, 1 << 20), label="seed")
+        names, cpu, pf, bpb, groups = setup(dev, n_layers=n_layers, nb=96, layout=layout, dtype=dtype,
+                                            two_groups=two, seed=seed)
+        rng = np.random.default_rng(seed)
+        blocks = metas_blocks(rng, n_meta, 96, two)
+        # a null id (block 0) only on load: a stored null page would leave its
+        # record bytes to whatever staging held, in the reference as here
+        load_blocks = list(blocks)
+        if data.draw(st.booleans(), label="null_block_on_load"):
+            load_blocks[0] = tuple([0] + list(g[1:]) for g in blocks[0])
+        layer_name = names[data.draw(st.integers(0, n_layers - 1), label="layer")] \
+            if data.draw(st.booleans(), label="layerwise") else None
+        host = torch.zeros(32 << 20, dtype=torch.uint8, pin_memory=True)
+        dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
+        ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * n_layers, dev_caches, host,
+                                staging_bytes=data.draw(st.sampled_from([320 << 10, 1 << 20, 8 << 20]),
+                                                        label="staging"))
+        offs, o = [], 4096
+        for b in blocks:
+            offs.append(o)
+            o += ctx.record_size(b, layer_name) + 512
+        saved = [int(x) for x in rng.integers(0, 1 << 40, n_meta)]
+        try:
+            ctx.store(offs, blocks, saved, layer_name=layer_name)
+        except RuntimeError as e:           # a meta larger than a staging half: refused up front
+            assert "staging half" in str(e)
+            return
+        shm = torch.zeros(32 << 20, dtype=torch.uint8)
+        okv.OracleKVIO(names, groups, bpb, [pf] * n_layers, cpu, shm).store(offs, blocks, saved,
+                                                                            layer_name=layer_name)
+        assert torch.equal(host, shm)
+        fresh_cpu = {n: torch.zeros_like(t) for n, t in cpu.items()}
+        fresh_dev = {n: to_dev(t, dev) for n, t in fresh_cpu.items()}
+        ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * n_layers, fresh_dev, host, staging_bytes=1 << 20)
+        got = ctx2.load(offs, load_blocks, layer_name=layer_name)
+        torch.cuda.synchronize()
+        want = okv.OracleKVIO(names, groups, bpb, [pf] * n_layers, fresh_cpu, shm).load(
+            offs, load_blocks, layer_name=layer_name)
+        assert got == want == saved
+        for n in names:
+            assert same_bytes(fresh_dev[n], fresh_cpu[n])
