@@ -135,6 +135,13 @@ def run_gpu(cfg, steps, warmup):
 
     fused = time_steps(step, steps, warmup, stream)
 
+    # the same 256 jobs as a plain scatter_pages (no rotation): the copy rate of
+    # this exact access pattern on this box, the ceiling the fused kernel meets
+    def pstep():
+        cp.scatter_pages(j["names"], j["offsets"], j["sizes"], idx, j["ioff"], stream.cuda_stream)
+
+    plain = time_steps(pstep, steps, warmup, stream)
+
     # return path: gather the whole request into [L, 2, T, H, D]
     T, L = w["T"], w["L"]
     out = torch.empty(L * 2 * T * cfg["kv_heads"] * cfg["head_dim"] * 2, dtype=torch.uint8, device=dev)
@@ -168,6 +175,7 @@ def run_gpu(cfg, steps, warmup):
     inplace = time_steps(rstep, steps, warmup, stream)
     inplace_bytes = sum(s[2] for s in segs) * L * cfg["kv_heads"] * cfg["head_dim"] * 2 * 2
     return dict(step_ms=fused["step_ms"], wall_s=fused["wall_s"], kern_ms=fused["kern_ms"],
+                p_kern_ms=plain["kern_ms"],
                 g_step_ms=gather["step_ms"], g_kern_ms=gather["kern_ms"], T=T, L=L,
                 r_step_ms=inplace["step_ms"], r_kern_ms=inplace["kern_ms"], r_bytes=inplace_bytes,
                 r_tokens=sum(s[2] for s in segs))
@@ -635,7 +643,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBPS, "traffic": read_traffic(),
                      "kernel": "scatter_rotate_lane_kernel<bf16,neox>", "kernel_ms": r["kern_ms"],
-                     "algorithmic_bytes": nbytes},
+                     "algorithmic_bytes": nbytes,
+                     "pattern_copy": {"kernel": "copy_pages_kernel<16,scatter> on the same jobs, no rotation",
+                                      "kernel_ms": r["p_kern_ms"], "GBps": _gbps(nbytes, r["p_kern_ms"]),
+                                      "fused_frac_of_it": achieved / _gbps(nbytes, r["p_kern_ms"])}},
         "gather": {"ms_per_step": r["g_step_ms"], "kernel_ms": r["g_kern_ms"],
                    "GBps": g_achieved, "frac": g_achieved / PEAK_HBM_GBPS,
                    "tokens_per_s": r["T"] / (r["g_step_ms"] / 1e3)},
