@@ -116,9 +116,20 @@ def test_fused_fp8(dev, layout, neox):
 
 
 def test_fused_llama3_8b_page_shape(dev):
-    # H=8, D=128 bf16 pages of 32 KiB, as the benchmark shape
+    # H=8, D=128 bf16 pages of 32 KiB, as the benchmark shape (two 16 KiB parts per page)
     fused_case(dev, "nhd", torch.bfloat16, True, 128, nb=40, h=8, d=128, L=2, seed=4,
                chunk_tokens=(128, 64, 40), deltas=(1024, 7168, 3))
+
+
+@pytest.mark.parametrize("layout,dtype,neox", [
+    ("pf", torch.bfloat16, True),        # 64 KiB K+V spans: four 16 KiB parts, K in the first two
+    ("pf_hnd", torch.bfloat16, False),   # head-major rows, four parts
+    ("pf", torch.uint8, True),           # 32 KiB fp8 K+V spans: two parts
+    ("hnd", torch.float16, True),        # 32 KiB head-major K pages: two parts
+])
+def test_fused_large_spans_in_parts(dev, layout, dtype, neox):
+    fused_case(dev, layout, dtype, neox, 128, nb=40, h=8, d=128, L=2, seed=12,
+               chunk_tokens=(128, 37, 40), deltas=(1024, -7168, 3))
 
 
 def test_fused_rejects_unaligned_rotary(dev):
