@@ -878,6 +878,14 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
                 path = kRotLane;
                 g.upr = static_cast<int32_t>(upr);
                 g.tok_div = static_cast<int32_t>(tok_div);
+                // page tiles in parts of at least 16 KiB (whole rows each): two
+                // halves of a 32 KiB bf16 K page measured ~1% faster at config 2
+                const int64_t units = L.PS * L.H * upr;
+                int lp = 0;
+                while ((units >> (lp + 1)) * 16 >= 16384 && units % (2ll << lp) == 0 &&
+                       (units >> (lp + 1)) % upr == 0)
+                    ++lp;
+                g.log2_parts = lp;
             }
         }
 
@@ -900,7 +908,7 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
             rs.delta = static_cast<float>(s.delta);
             rs.tile_begin = static_cast<int32_t>(tiles);
             if (path == kRotLane)
-                tiles += last_block - s.tok_start / L.PS + 1;   // the pages the segment touches
+                tiles += (last_block - s.tok_start / L.PS + 1) << g.log2_parts;   // the pages the segment touches
             else
                 tiles += (s.n_tokens + g.tile_tokens - 1) / g.tile_tokens;
             segs.push_back(rs);
