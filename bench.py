@@ -607,7 +607,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print("bench.py measures one GPU: the KV-reuse hot path is per-GPU work with no "
-              "cross-GPU exchange (see DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "cross-GPU exchange; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     cfg = CFG2
     r = run_gpu(cfg, a.steps, a.warmup)
