@@ -15,7 +15,8 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libdaric_cache_ops.so")
 MAX_DIMS = 8
-ABI_VERSION = 3
+ABI_VERSION = 4
+ERR_VALUE = 5
 
 DTYPE_CODES = {
     torch.uint8: 0,
@@ -112,12 +113,14 @@ def load() -> ctypes.CDLL:
 
 
 def check(status: int) -> None:
-    """Raises RuntimeError with the library's message for a non-zero status
-    (TORCH_CHECK and std::runtime_error both surface as RuntimeError in the
-    reference's pybind11 module)."""
+    """Raises the library's message for a non-zero status: RuntimeError, as
+    TORCH_CHECK and std::runtime_error surface in the reference's pybind11
+    module, or ValueError for the cache layouts the reference's rotation
+    rejects with ValueError (daric/adaption/adapter.py:20-27, 336-368)."""
     if status != 0:
         msg = load().daric_last_error()
-        raise RuntimeError(msg.decode() if msg else f"daric error {status}")
+        text = msg.decode() if msg else f"daric error {status}"
+        raise (ValueError if status == ERR_VALUE else RuntimeError)(text)
 
 
 def desc(t: torch.Tensor) -> DaricTensor:

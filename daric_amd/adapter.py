@@ -10,10 +10,20 @@ and one rerotate_pages call covers every layer that shares a cache geometry
 and rotary embedding; cos/sin are formed from the rotary inverse frequencies
 in registers on the GPU.
 
-The layer topology the reference reads from the process-global
-ProcessLocalConfig.cache_topo (configs/engine.py:11-70) is passed to the
-constructor instead (any object with get_all_layer_names(),
-get_group_idx(name) and layers[name].page_first).
+Layer topology. The reference reads the process-global
+ProcessLocalConfig.cache_topo (configs/engine.py:11-70, 73-161) at
+construction and again at every rotation (adapter.py:94, 154, 241, 311), and
+is built as Adapter(config.adaption_config) (cache_engine.py:260). Built that
+way here, the adapter does the same: it imports daric.configs and reads
+ProcessLocalConfig.cache_topo at each use, so the page_first flags that
+finish_register_process_local_config sets after construction
+(integration/vllm/utils.py:212-220) are seen. Outside DARIC, pass the
+topology as `cache_topo` (any object with get_all_layer_names(),
+get_group_idx(name) and layers[name].page_first); with neither, the
+constructor raises.
+
+Bad cache layouts raise ValueError with the reference's text
+(adapter.py:20-27, 336-368), before any layer is touched.
 """
 from __future__ import annotations
 
@@ -27,7 +37,7 @@ from . import cache_ops
 from .policy import DARICPolicy
 
 __all__ = ["AdaptionConfig", "LayerCacheTopo", "CacheTopo", "Adapter", "plan_load_segments",
-           "plan_multi_segments"]
+           "plan_multi_segments", "check_rerotate_layout"]
 
 
 @dataclass
@@ -127,10 +137,52 @@ def _inv_freq(rotary) -> torch.Tensor:
     return torch.as_tensor(inv).detach().to(torch.float32).reshape(-1)
 
 
+def check_rerotate_layout(layer_name: str, kv: torch.Tensor, page_first: bool, rotary_dim: int) -> None:
+    """The layouts the reference's rotation accepts (adapter.py:20-27 for the
+    rank, 336-350 for packed 4-D caches); anything else raises ValueError with
+    the reference's message."""
+    if kv.ndim not in (3, 4, 5):
+        raise ValueError(f"Unsupported KV cache rank for rerotate: {kv.ndim}")
+    if kv.ndim != 4:
+        return
+    width = int(kv.shape[3])
+    if not page_first:
+        why = "page_first must be true"
+    elif width <= 0 or width % 2:
+        why = "packed content dimension must be positive and even"
+    elif kv.stride(3) != 1:
+        why = "packed content feature stride must equal 1"
+    elif rotary_dim <= 0 or rotary_dim % 2 or rotary_dim > width // 2:
+        why = "rotary_dim must be positive, even, and no greater than the packed K head dimension"
+    else:
+        return
+    raise ValueError(f"Invalid 4D KV cache for rerotate: layer={layer_name}, shape={tuple(kv.shape)}, "
+                     f"stride={tuple(kv.stride())}, dtype={kv.dtype}, rotary_dim={rotary_dim}, "
+                     f"constraint={why}")
+
+
+def _process_local_config():
+    """DARIC's ProcessLocalConfig class, whose cache_topo attribute holds the
+    worker's layer topology; RuntimeError when it is not available."""
+    try:
+        from daric.configs import ProcessLocalConfig
+    except ImportError as e:
+        raise RuntimeError(
+            "Adapter(config) reads the layer topology from daric.configs.ProcessLocalConfig.cache_topo, "
+            f"but daric.configs cannot be imported ({e}); pass cache_topo= explicitly") from e
+    if getattr(ProcessLocalConfig, "cache_topo", None) is None:
+        raise RuntimeError(
+            "Adapter(config) reads the layer topology from daric.configs.ProcessLocalConfig.cache_topo, "
+            "which is not set yet; construct the Adapter after the process-local config is registered, "
+            "or pass cache_topo= explicitly")
+    return ProcessLocalConfig
+
+
 class Adapter:
     def __init__(self, config: AdaptionConfig, cache_topo=None):
         self.config = config
-        self.cache_topo = cache_topo if cache_topo is not None else CacheTopo()
+        self._topo = cache_topo
+        self._plc = _process_local_config() if cache_topo is None else None
         self.num_layers = len(self.cache_topo.get_all_layer_names())
         self.kvcaches: dict = {}
         self.rotary_embeds: dict = {}
@@ -141,6 +193,11 @@ class Adapter:
         else:
             self.recompute_policy = None
         self.rerotate = config.rerotate
+
+    @property
+    def cache_topo(self):
+        """The explicit topology, else ProcessLocalConfig.cache_topo as it is now."""
+        return self._topo if self._topo is not None else self._plc.cache_topo
 
     # ------------------------------------------------------------ registration
     def register_kvcaches(self, kvcaches: dict) -> None:
@@ -166,25 +223,32 @@ class Adapter:
         """Runs `plan(group_idx) -> (block table, segments)` for every KV-cache
         group and rotates the group's layers, batching the layers that share a
         geometry and a rotary embedding into one call."""
+        topo = self.cache_topo
         by_group: dict = {}
         for name in layer_names:
             if name in self.kvcaches:
-                by_group.setdefault(self.cache_topo.get_group_idx(name), []).append(name)
+                by_group.setdefault(topo.get_group_idx(name), []).append(name)
+        work = []
         for group_idx, names in by_group.items():
             bt, segs = plan(group_idx)
             if not segs:
                 continue
-            first = self.kvcaches[names[0]]
-            device = first.device
-            bt_dev = torch.from_numpy(bt).to(device, non_blocking=True)
+            kv0 = self.kvcaches[names[0]]
+            if kv0.ndim not in (3, 4, 5):      # the reference sizes pages from the first layer
+                raise ValueError(f"Unsupported KV cache rank for rerotate: {kv0.ndim}")
             batches: dict = {}
             for name in names:
                 kv = self.kvcaches[name]
                 rotary = self.rotary_embeds[name]
-                page_first = bool(self.cache_topo.layers[name].page_first)
+                page_first = bool(topo.layers[name].page_first)
+                check_rerotate_layout(name, kv, page_first, int(rotary.rotary_dim))
                 key = (tuple(kv.shape), kv.stride(), kv.dtype, page_first, id(rotary),
                        int(rotary.rotary_dim), bool(rotary.is_neox_style))
                 batches.setdefault(key, (rotary, page_first, []))[2].append(kv)
+            work.append((kv0.device, bt, segs, batches))
+        # every layout is checked before any layer is rotated
+        for device, bt, segs, batches in work:
+            bt_dev = torch.from_numpy(bt).to(device, non_blocking=True)
             for rotary, page_first, kvs in batches.values():
                 cache_ops.rerotate_pages(kvs, page_first, bt_dev, segs,
                                          self._device_inv_freq(rotary, device),

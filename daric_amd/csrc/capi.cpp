@@ -171,7 +171,7 @@ RopeLayout rope_layout(const daric_tensor& t, bool page_first, int rotary_dim) {
         if (!constraint && (rotary_dim <= 0 || rotary_dim % 2 != 0 || rotary_dim > hd))
             constraint = "rotary_dim must be positive, even, and no greater than the packed K head dimension";
         if (constraint)
-            throw Error(DARIC_ERR_INVALID,
+            throw Error(DARIC_ERR_VALUE,
                         cat("Invalid 4D KV cache for rerotate: shape=", sizes_str(t), ", stride=",
                             strides_str(t), ", rotary_dim=", rotary_dim, ", constraint=", constraint));
         r.PS = t.sizes[2]; r.H = t.sizes[1]; r.D = hd;
@@ -185,7 +185,7 @@ RopeLayout rope_layout(const daric_tensor& t, bool page_first, int rotary_dim) {
         r.row_width = r.D;
         DARIC_CHECK(t.strides[2] == 1 || r.D == 1, "KV cache hidden stride must equal 1 for rerotate");
     } else {
-        throw Error(DARIC_ERR_INVALID, cat("Unsupported KV cache rank for rerotate: ", t.ndim));
+        throw Error(DARIC_ERR_VALUE, cat("Unsupported KV cache rank for rerotate: ", t.ndim));
     }
     DARIC_CHECK(rotary_dim > 0 && rotary_dim % 2 == 0 && rotary_dim <= r.D,
                 "rotary_dim must be positive, even and no greater than head_dim (", r.D,

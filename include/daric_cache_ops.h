@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DARIC_ABI_VERSION 3
+#define DARIC_ABI_VERSION 4
 
 /* Status codes. */
 #define DARIC_OK 0
@@ -42,6 +42,8 @@ extern "C" {
 #define DARIC_ERR_RUNTIME 2   /* std::runtime_error in the reference (e.g. byte_size mismatch) */
 #define DARIC_ERR_HIP 3       /* a HIP runtime call failed */
 #define DARIC_ERR_NOMEM 4     /* host allocation failed */
+#define DARIC_ERR_VALUE 5     /* a cache layout the rotation does not accept (reference: ValueError,
+                                 daric/adaption/adapter.py:20-27, 336-368) */
 
 /* Element type codes carried by daric_tensor.dtype. */
 #define DARIC_DTYPE_UINT8 0

@@ -59,7 +59,7 @@ def test_exports_every_declared_symbol(lib):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover the header"
-    assert lib.daric_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.daric_abi_version() == _lib.ABI_VERSION == 4
 
 
 def fake(shape, dtype, device=0, strides=None, ptr=0x10000000):
@@ -243,13 +243,25 @@ def test_rerotate_layout_errors(lib):
         arr = (_lib.DaricTensor * 1)(fake(shape, dtype))
         st = lib.daric_rerotate_pages(arr, 1, pf, ctypes.byref(bt), seg, 1, ctypes.byref(rope), None,
                                       ctypes.c_uint64(0))
-        return lib.daric_last_error().decode() if st else None
+        if not st:
+            return None
+        msg = lib.daric_last_error().decode()
+        # the layouts the reference's rotation rejects with ValueError carry their
+        # own status, which the Python wrapper raises as ValueError
+        with pytest.raises(ValueError if st == _lib.ERR_VALUE else RuntimeError, match=re.escape(msg)):
+            _lib.check(st)
+        return st, msg
 
-    assert "page_first must be true" in run((8, 2, 4, 32), 0)
-    assert "rotary_dim must be positive, even, and no greater" in run((8, 2, 4, 32), 1, rd=32)
-    assert "Unsupported KV cache rank for rerotate: 2" in run((8, 32), 1)
-    assert "unsupported KV cache dtype" in run((2, 8, 4, 2, 16), 0, dtype=torch.float32)
-    assert "reads past the end of block_table" in run((2, 8, 4, 2, 16), 0, nseg_tokens=17)
+    assert run((8, 2, 4, 32), 0) == (
+        _lib.ERR_VALUE, "Invalid 4D KV cache for rerotate: shape=[8, 2, 4, 32], stride=[256, 128, 32, 1], "
+        "rotary_dim=16, constraint=page_first must be true")
+    st, msg = run((8, 2, 4, 32), 1, rd=32)
+    assert st == _lib.ERR_VALUE and "rotary_dim must be positive, even, and no greater" in msg
+    assert run((8, 32), 1) == (_lib.ERR_VALUE, "Unsupported KV cache rank for rerotate: 2")
+    st, msg = run((2, 8, 4, 2, 16), 0, dtype=torch.float32)
+    assert st == 1 and "unsupported KV cache dtype" in msg
+    st, msg = run((2, 8, 4, 2, 16), 0, nseg_tokens=17)
+    assert st == 1 and "reads past the end of block_table" in msg
 
 
 def test_host_fp8_conversion_matches_oracle(hosttest):
