@@ -81,6 +81,9 @@ SIGNATURES = {
                                             c_int64, c_uint64]),
     "daric_copier_scatter_pages_rerotate": (c_int, [c_void_p, STRS, c_int64, I64P, c_int64, I64P, c_int64, T,
                                                     I64P, c_int64, I64P, I64P, P(DaricRope), c_uint64]),
+    "daric_copier_scatter_pages_rerotate_noalloc": (c_int, [c_void_p, STRS, c_int64, I64P, c_int64, I64P,
+                                                            c_int64, T, I64P, c_int64, I64P, I64P,
+                                                            P(DaricRope), c_uint64]),
     "daric_batched_memcpy_d2h": (c_int, [T, T, I64P, I64P, I64P, c_int64, c_uint64]),
     "daric_batched_memcpy_h2d": (c_int, [T, T, I64P, I64P, I64P, c_int64, c_uint64]),
     "daric_rerotate_pages": (c_int, [T, c_int64, c_int, T, P(DaricRopeSegment), c_int64, P(DaricRope), T,

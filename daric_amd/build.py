@@ -23,7 +23,7 @@ LIB = os.path.join(LIBDIR, "libdaric_cache_ops.so")
 HOSTTEST_LIB = os.path.join(LIBDIR, "libdaric_hosttest.so")
 
 SOURCES = ["capi.cpp", "runtime.cpp", "copy_kernels.hip", "rope_kernels.hip", "select_kernels.hip",
-           "token_kernels.hip"]
+           "token_kernels.hip", "noalloc.hip"]
 
 ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wshadow", "-Wno-unused-result",

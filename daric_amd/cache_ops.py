@@ -192,6 +192,26 @@ class CacheCopier:
                                stream: int = 0) -> None:
         """scatter_pages + re-rotation of the first num_tokens[i] tokens of job
         i by deltas[i] positions, in one pass (see include/daric_cache_ops.h)."""
+        self._fused(self._lib.daric_copier_scatter_pages_rerotate, layer_names, offsets, byte_sizes,
+                    indices_flat, indices_offsets, deltas, num_tokens, inv_freq, rotary_dim,
+                    is_neox_style, stream)
+
+    def scatter_pages_rerotate_noalloc(self, layer_names: Sequence[str], offsets: Sequence[int],
+                                       byte_sizes: Sequence[int], indices_flat: torch.Tensor,
+                                       indices_offsets: Sequence[int], deltas: Sequence[int],
+                                       num_tokens: Sequence[int], inv_freq: torch.Tensor,
+                                       rotary_dim: int, is_neox_style: bool = True,
+                                       stream: int = 0) -> None:
+        """scatter_pages_rerotate without allocating device or pinned memory:
+        large job lists are staged in a static per-GPU array of 3276 jobs.
+        Calls that overlap on one GPU race on that array (see
+        include/daric_cache_ops.h). No counterpart in the reference."""
+        self._fused(self._lib.daric_copier_scatter_pages_rerotate_noalloc, layer_names, offsets,
+                    byte_sizes, indices_flat, indices_offsets, deltas, num_tokens, inv_freq,
+                    rotary_dim, is_neox_style, stream)
+
+    def _fused(self, fn, layer_names, offsets, byte_sizes, indices_flat, indices_offsets, deltas,
+               num_tokens, inv_freq, rotary_dim, is_neox_style, stream):
         names = list(layer_names)
         if len(deltas) != len(names) or len(num_tokens) != len(names):
             if names:
@@ -199,8 +219,8 @@ class CacheCopier:
         dev = self._device(names)
         rope = _rope(inv_freq, rotary_dim, is_neox_style, dev) if names else DaricRope()
         dl, nt = I64(deltas), I64(num_tokens)
-        self._copy(self._lib.daric_copier_scatter_pages_rerotate, names, offsets, byte_sizes,
-                   indices_flat, indices_offsets, stream, extra=(dl.ptr, nt.ptr, ctypes.byref(rope)))
+        self._copy(fn, names, offsets, byte_sizes, indices_flat, indices_offsets, stream,
+                   extra=(dl.ptr, nt.ptr, ctypes.byref(rope)))
         if names and dev is not None:
             _record(_resolve_stream(stream, dev), dev, inv_freq)
 

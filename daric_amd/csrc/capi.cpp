@@ -647,13 +647,19 @@ int daric_copier_scatter_tokens(daric_copier* c, const char* const* names, int64
                        indices_offsets, n_indices_offsets, stream, false);
 }
 
-int daric_copier_scatter_pages_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs,
-                                        const int64_t* offsets, int64_t n_offsets,
-                                        const int64_t* byte_sizes, int64_t n_byte_sizes,
-                                        const daric_tensor* indices,
-                                        const int64_t* indices_offsets, int64_t n_indices_offsets,
-                                        const int64_t* deltas, const int64_t* num_tokens,
-                                        const daric_rope* rope, uint64_t stream) {
+}  // extern "C"
+
+namespace {
+
+// scatter_pages_rerotate and its allocation-free variant: the same checks
+// and kernels; they differ only in how the job descriptors reach the kernels
+// when they do not fit in the kernel arguments (the ring, or the static
+// scratch array).
+int scatter_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs, const int64_t* offsets,
+                     int64_t n_offsets, const int64_t* byte_sizes, int64_t n_byte_sizes,
+                     const daric_tensor* indices, const int64_t* indices_offsets, int64_t n_indices_offsets,
+                     const int64_t* deltas, const int64_t* num_tokens, const daric_rope* rope,
+                     uint64_t stream, bool noalloc) {
     return guarded([&] {
         DARIC_CHECK(c != nullptr, "copier must not be null");
         std::lock_guard<std::mutex> lk(c->mu);
@@ -715,8 +721,22 @@ int daric_copier_scatter_pages_rerotate(daric_copier* c, const char* const* name
             grp->jobs.push_back(j);
             grp->max_tiles = std::max<int64_t>(grp->max_tiles, int64_t(j.prefix) * j.n_sel);
         }
+        // Allocation-free variant: job sets that do not travel inline are
+        // staged in the static scratch array, one region per launch group.
+        size_t staged = 0;
+        if (noalloc) {
+            for (const Group& gr : groups) {
+                const size_t b = gr.jobs.size() * sizeof(CopyJob);
+                if (gr.max_tiles > 0 && b > static_cast<size_t>(kInlineDescBytes)) staged += (b + 255) / 256 * 256;
+            }
+            DARIC_CHECK(staged <= kNoAllocScratchBytes, "scatter_pages_rerotate_noalloc: the jobs' descriptors need ",
+                        staged, " bytes of scratch, more than the ", kNoAllocScratchBytes, " bytes (",
+                        kNoAllocScratchBytes / sizeof(CopyJob), " jobs) it holds; split the call");
+        }
         DeviceGuard guard(r.device);
         const hipStream_t st = as_stream(stream);
+        uint8_t* scratch = staged > 0 ? noalloc_scratch(r.device) : nullptr;
+        size_t scratch_off = 0;
         for (const Group& gr : groups) {
             if (gr.max_tiles == 0) continue;
             RowGeomDiv gd;
@@ -724,17 +744,59 @@ int daric_copier_scatter_pages_rerotate(daric_copier* c, const char* const* name
             gd.ipr = FastDiv(gd.g.ipr);
             gd.tok_div = FastDiv(gd.g.tok_div);
             gd.ps = FastDiv(gd.g.PS);
+            const size_t bytes = gr.jobs.size() * sizeof(CopyJob);
+            if (noalloc) {
+                DescArg arg;
+                arg.ptr = nullptr;
+                arg.reserved = 0;
+                if (bytes <= static_cast<size_t>(kInlineDescBytes)) {
+                    std::memcpy(arg.inl, gr.jobs.data(), bytes);
+                } else {
+                    stash_descriptors(gr.jobs.data(), bytes, scratch + scratch_off, st);
+                    arg.ptr = scratch + scratch_off;
+                    scratch_off += (bytes + 255) / 256 * 256;
+                }
+                launch_scatter_rotate(arg, static_cast<int>(gr.jobs.size()), static_cast<int>(gr.max_tiles),
+                                      gd, gr.kind, rope->is_neox != 0, rope->inv_freq, st);
+                continue;
+            }
             // Job sets too large to travel inline are read by the fused
             // kernels straight from the pinned slot (one 80-byte read per
             // 32 KiB workgroup): no upload kernel and no dependency gap before
             // them, ~4 us less per call on MI355X. The copy kernels keep the
             // upload: their 8 KiB workgroups are 4x as many, and reading over
             // the host link cost the gather ~5 us.
-            DescHandOver ho(r.device, gr.jobs.data(), gr.jobs.size() * sizeof(CopyJob), st, true);
+            DescHandOver ho(r.device, gr.jobs.data(), bytes, st, true);
             launch_scatter_rotate(ho.arg(), static_cast<int>(gr.jobs.size()), static_cast<int>(gr.max_tiles),
                                   gd, gr.kind, rope->is_neox != 0, rope->inv_freq, st);
         }
     });
+}
+
+}  // namespace
+
+extern "C" {
+
+int daric_copier_scatter_pages_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs,
+                                        const int64_t* offsets, int64_t n_offsets,
+                                        const int64_t* byte_sizes, int64_t n_byte_sizes,
+                                        const daric_tensor* indices,
+                                        const int64_t* indices_offsets, int64_t n_indices_offsets,
+                                        const int64_t* deltas, const int64_t* num_tokens,
+                                        const daric_rope* rope, uint64_t stream) {
+    return scatter_rerotate(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices,
+                            indices_offsets, n_indices_offsets, deltas, num_tokens, rope, stream, false);
+}
+
+int daric_copier_scatter_pages_rerotate_noalloc(daric_copier* c, const char* const* names, int64_t n_jobs,
+                                                const int64_t* offsets, int64_t n_offsets,
+                                                const int64_t* byte_sizes, int64_t n_byte_sizes,
+                                                const daric_tensor* indices,
+                                                const int64_t* indices_offsets, int64_t n_indices_offsets,
+                                                const int64_t* deltas, const int64_t* num_tokens,
+                                                const daric_rope* rope, uint64_t stream) {
+    return scatter_rerotate(c, names, n_jobs, offsets, n_offsets, byte_sizes, n_byte_sizes, indices,
+                            indices_offsets, n_indices_offsets, deltas, num_tokens, rope, stream, true);
 }
 
 // ------------------------------------------------------------ batched memcpy

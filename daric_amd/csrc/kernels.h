@@ -136,6 +136,15 @@ void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g
 // (descriptor upload; both 16-byte aligned).
 void launch_upload(const void* src, void* dst, size_t n16, hipStream_t stream);
 
+// Allocation-free descriptor staging (noalloc.hip). Each GPU holds a static
+// device array of kNoAllocScratchBytes; noalloc_scratch returns its address on
+// `device` (looked up once per device). stash_descriptors enqueues kernels on
+// `stream` that write `bytes` (a multiple of 16) from host memory `src` to
+// `dst` in that array, carrying them in their kernel arguments.
+constexpr size_t kNoAllocScratchBytes = 256 * 1024;
+uint8_t* noalloc_scratch(int device);
+void stash_descriptors(const void* src, size_t bytes, uint8_t* dst, hipStream_t stream);
+
 // Launch-configuration error check after a <<<>>> launch.
 void check_launch(const char* what);
 

@@ -172,6 +172,30 @@ int daric_copier_scatter_pages_rerotate(daric_copier* copier,
                                         const int64_t* deltas, const int64_t* num_tokens,
                                         const daric_rope* rope, uint64_t stream);
 
+/* Allocation-free variant of daric_copier_scatter_pages_rerotate: the same
+ * arguments, checks, kernels and results. No counterpart in the reference;
+ * it is for callers that cannot allocate: code under HIP stream capture,
+ * serving loops with a fixed memory budget, harnesses that forbid hipMalloc.
+ * Where daric_copier_scatter_pages_rerotate stages a job list too large for
+ * the kernel arguments in its descriptor ring (pinned host and device memory
+ * that it allocates on first use), this entry point stages it in a static
+ * device array of 262144 bytes per GPU (3276 jobs of 80 bytes), carried there
+ * by kernels whose arguments hold the bytes. It calls no hipMalloc, hipFree
+ * or hipHostMalloc and enqueues only kernels. A call whose jobs need more
+ * than the array holds returns DARIC_ERR_INVALID before any device work.
+ * Every call on one GPU uses that GPU's array, which keeps the last call's
+ * descriptors: calls that overlap on one GPU (on different streams, or
+ * graphs replayed concurrently) race on it, and the caller must order them. */
+int daric_copier_scatter_pages_rerotate_noalloc(daric_copier* copier,
+                                                const char* const* layer_names, int64_t n_jobs,
+                                                const int64_t* offsets, int64_t n_offsets,
+                                                const int64_t* byte_sizes, int64_t n_byte_sizes,
+                                                const daric_tensor* indices_flat,
+                                                const int64_t* indices_offsets,
+                                                int64_t n_indices_offsets,
+                                                const int64_t* deltas, const int64_t* num_tokens,
+                                                const daric_rope* rope, uint64_t stream);
+
 /* Token-major gather: like gather_pages, but job i's store range holds the
  * selected pages' rows token by token, [n_kv][n_sel * PS][H][D] (K rows, then
  * V rows; n_kv = 1 for a 3-D MLA cache), whatever the cache layout: NHD

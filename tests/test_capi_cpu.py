@@ -264,6 +264,31 @@ def test_rerotate_layout_errors(lib):
     assert st == 1 and "reads past the end of block_table" in msg
 
 
+def test_noalloc_rejects_job_lists_beyond_its_scratch(lib):
+    """The allocation-free fused entry point stages descriptors in a static
+    262144-byte array per GPU: 3276 jobs of 80 bytes fit; one more is refused
+    before any device work (every pointer here is fake)."""
+    c = CCopier(lib)
+    span = 16 * 8 * 128 * 2
+    assert c.register_layer("L", fake((2, 8, 16, 8, 128), torch.bfloat16), 0) is None
+    assert c.register_store(fake((2 * span,), torch.uint8, ptr=0x30000000)) is None
+    idx = fake((1,), torch.int32, ptr=0x20000000)
+    rope = _lib.DaricRope(0x40000000, 64, 1)
+
+    def run(n):
+        names = ["L"] * n
+        sizes = [2 * span] + [0] * (n - 1)          # job 0 moves one page, the others none
+        off, sz, io = _lib.I64([0] * n), _lib.I64(sizes), _lib.I64([0] + [1] * n)
+        dl, nt = _lib.I64([5] * n), _lib.I64([16] * n)
+        st = lib.daric_copier_scatter_pages_rerotate_noalloc(
+            c.h, _lib.str_array(names), n, off.ptr, off.n, sz.ptr, sz.n, ctypes.byref(idx), io.ptr, io.n,
+            dl.ptr, nt.ptr, ctypes.byref(rope), ctypes.c_uint64(0))
+        return st, lib.daric_last_error().decode()
+
+    st, msg = run(3277)
+    assert st == 1 and "need 262400 bytes of scratch, more than the 262144 bytes (3276 jobs)" in msg
+
+
 def test_host_fp8_conversion_matches_oracle(hosttest):
     rng = np.random.default_rng(0)
     vals = np.concatenate([

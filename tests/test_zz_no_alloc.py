@@ -1,0 +1,109 @@
+"""The allocation-free fused scatter + re-rotation
+(daric_copier_scatter_pages_rerotate_noalloc), called through the C ABI,
+against the existing entry point (daric_copier_scatter_pages_rerotate) on
+the same inputs: bit-exact, on calls in a row whose job lists shrink (the
+static scratch array keeps the previous call's descriptors), with two launch
+groups staged in one call, and with a job list small enough to travel in the
+kernel arguments. Device memory stays unallocated across the calls."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from daric_amd import _lib, cache_ops
+from tests.gpu_util import same_bytes
+
+pytestmark = pytest.mark.gpu
+
+NB, PS, H = 96, 16, 8
+
+
+def make_layers(dev, dims, gen):
+    return [torch.randn(2, NB, PS, H, d, generator=gen).to(torch.bfloat16).to(dev) for d in dims]
+
+
+def plan(n_layers, chunks, span_of, rng):
+    """Jobs of gpu_kv_io._build_copy_plan order: for each chunk, for each layer."""
+    names, offsets, sizes, flat, ioff, deltas, ntok = [], [], [], [], [0], [], []
+    off = 0
+    for pages in chunks:
+        d = int(rng.integers(-3000, 3000))
+        n = int(rng.integers(1, len(pages) * PS + 1))
+        for l in range(n_layers):
+            names.append(f"model.layers.{l}.self_attn.attn")
+            offsets.append(off)
+            sz = 2 * len(pages) * span_of(l)
+            sizes.append(sz)
+            flat.extend(pages)
+            ioff.append(len(flat))
+            deltas.append(d)
+            ntok.append(n)
+            off += sz
+    return names, offsets, sizes, flat, ioff, deltas, ntok, off
+
+
+def call(lib, fn, copier, names, offsets, sizes, idx, ioff, deltas, ntok, rope, stream):
+    off, sz, io = _lib.I64(offsets), _lib.I64(sizes), _lib.I64(ioff)
+    dl, nt = _lib.I64(deltas), _lib.I64(ntok)
+    ix = _lib.desc(idx)
+    return fn(copier._h, _lib.str_array(names), len(names), off.ptr, off.n, sz.ptr, sz.n,
+              ctypes.byref(ix), io.ptr, io.n, dl.ptr, nt.ptr, ctypes.byref(rope), ctypes.c_uint64(stream))
+
+
+def test_noalloc_matches_fused_entry_point(dev):
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(7)
+    rng = np.random.default_rng(7)
+    dims = [128] * 4 + [64] * 4                       # two row geometries: two launch groups
+    base = make_layers(dev, dims, gen)
+    span_of = lambda l: PS * H * dims[l] * 2       # bytes of one page's K (or V) half
+    inv = (1.0 / (500000.0 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))).to(dev)
+    rope = _lib.DaricRope()
+    rope.inv_freq = inv.data_ptr()
+    rope.rotary_dim = 64
+    rope.is_neox = 1
+
+    copiers, outs = [], []
+    for _ in range(2):
+        c = cache_ops.CacheCopier()
+        layers = [t.clone() for t in base]
+        for l, t in enumerate(layers):
+            c.register_layer(f"model.layers.{l}.self_attn.attn", t, False)
+        copiers.append(c)
+        outs.append(layers)
+
+    perm = (rng.permutation(NB - 1) + 1).tolist()
+    # Per launch group (4 layers each): 12 chunks x 4 = 48 jobs (3840
+    # descriptor bytes, over the 2816-byte inline limit: staged), then
+    # 9 x 4 = 36 jobs (2880 bytes, staged, smaller), then 2 x 4 = 8 jobs
+    # (640 bytes, inline). Chunks never share a page.
+    calls = [[perm[3 * i: 3 * i + 3] for i in range(12)],
+             [perm[40 + 2 * i: 42 + 2 * i] for i in range(9)],
+             [perm[60:63], [perm[63]]]]
+    side = torch.cuda.Stream()
+    for k, chunks in enumerate(calls):
+        names, offsets, sizes, flat, ioff, deltas, ntok, total = plan(len(dims), chunks, span_of, rng)
+        staging = torch.randint(-128, 127, (total,), dtype=torch.int8, generator=gen).view(torch.uint8).to(dev)
+        idx = torch.tensor(flat, dtype=torch.int32, device=dev)
+        for c in copiers:
+            c.register_store(staging)
+        torch.cuda.synchronize()
+        st = call(lib, lib.daric_copier_scatter_pages_rerotate, copiers[0], names, offsets, sizes, idx,
+                  ioff, deltas, ntok, rope, torch.cuda.current_stream().cuda_stream)
+        assert st == 0, lib.daric_last_error()
+        torch.cuda.synchronize()
+        # The first call also sets up the side stream in the HIP runtime (its
+        # first launch there took 2 MiB of device memory on MI355X); the later
+        # calls must take none: the ring's device half alone would be 16 MiB.
+        free_before = torch.cuda.mem_get_info()[0]
+        st = call(lib, lib.daric_copier_scatter_pages_rerotate_noalloc, copiers[1], names, offsets, sizes,
+                  idx, ioff, deltas, ntok, rope, side.cuda_stream)
+        assert st == 0, lib.daric_last_error()
+        torch.cuda.synchronize()
+        if k > 0:
+            assert torch.cuda.mem_get_info()[0] == free_before, f"call {k} took device memory"
+        for l in range(len(dims)):
+            assert same_bytes(outs[1][l], outs[0][l]), f"call {k} layer {l}"
+    # both paths really rotated something
+    assert not same_bytes(outs[0][0], base[0])
