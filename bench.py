@@ -205,16 +205,13 @@ def _student_t(shape, df, gen, device):
     return z / torch.sqrt(chi / df)
 
 
-def run_config3(steps, warmup, seed=0):
-    """Batched selective recompute: 32 requests x 6 chunks x
-    512 tokens = 98304 tokens, Llama-3-8B KV shape, bf16. Chunk pages come from
-    a seeded permutation of the block pool and each request's chunk order is
-    shuffled by seed. Recomputed K = cached K + 0.1 * StudentT(3). One step =
-    kv_deviation + topk_per_chunk (k = 77 of 512) + merge_rows of the selected
-    K/V rows."""
-    from daric_amd import cache_ops
+def config3_inputs(dev, seed=0):
+    """BASELINE config 3's inputs: 32 requests x 6 chunks x 512 tokens = 98304
+    tokens, Llama-3-8B KV shape, bf16. Chunk pages come from a seeded
+    permutation of the block pool and each request's chunk order is shuffled by
+    seed. Recomputed K = cached K + 0.1 * StudentT(3); recomputed V ~ N(0,1);
+    k = 77 of 512 per chunk."""
     c = CFG3
-    dev = torch.device("cuda:0")
     L, H, D, PS = c["layers"], c["kv_heads"], c["head_dim"], c["block_size"]
     n_chunk = c["requests"] * c["chunks"]
     T = n_chunk * c["chunk_tokens"]
@@ -239,6 +236,19 @@ def run_config3(steps, warmup, seed=0):
         base = layers[l][0][slot_blk, slot_in].float()
         k_new[l] = (base + c["noise_scale"] * _student_t(base.shape, c["t_df"], gd, dev)).to(torch.bfloat16)
     v_new = torch.randn(L, T, H, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    return dict(L=L, H=H, D=D, PS=PS, NB=NB, T=T, n_chunk=n_chunk, k=k, layers=layers, bt=bt,
+                chunks=chunks, k_new=k_new, v_new=v_new)
+
+
+def run_config3(steps, warmup, seed=0):
+    """Batched selective recompute (config3_inputs). One
+    step = kv_deviation + topk_per_chunk (k = 77 of 512) + merge_rows of the
+    selected K/V rows."""
+    from daric_amd import cache_ops
+    dev = torch.device("cuda:0")
+    w = config3_inputs(dev, seed)
+    L, H, D, T, k, n_chunk = w["L"], w["H"], w["D"], w["T"], w["k"], w["n_chunk"]
+    layers, bt, chunks, k_new, v_new = w["layers"], w["bt"], w["chunks"], w["k_new"], w["v_new"]
     keys = torch.empty(L, T, dtype=torch.float32, device=dev)
     sel = torch.empty(L, n_chunk, k, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
@@ -275,8 +285,9 @@ def run_config3(steps, warmup, seed=0):
                                           GBps=_gbps(dev_bytes, parts["deviation"])),
                         "topk": dict(ms=parts["topk"], bytes=topk_bytes),
                         "merge": dict(ms=parts["merge"], bytes=merge_bytes,
-                                      GBps=_gbps(merge_bytes, parts["merge"]))})
-    del layers, k_new, v_new, keys, sel
+                                      GBps=_gbps(merge_bytes, parts["merge"]),
+                                      frac=_gbps(merge_bytes, parts["merge"]) / PEAK_HBM_GBPS)})
+    del w, layers, k_new, v_new, keys, sel
     torch.cuda.empty_cache()
     return out
 
@@ -327,6 +338,34 @@ def run_config2_hnd(steps, warmup, seed=0):
     return out
 
 
+def config4_inputs(dev, seed=0):
+    """BASELINE config 4's inputs: 65536 tokens (4096 pages) of a Llama-3-8B bf16
+    cache ([2, 8192, 16, 8, 128] per layer, 32 layers, N(0,1)) chosen by a
+    seeded random block table (the null block excluded)."""
+    c = CFG4
+    L, H, D, PS, NB = c["layers"], c["kv_heads"], c["head_dim"], c["block_size"], c["num_blocks"]
+    T = c["tokens"]
+    n_pages = T // PS
+    g = torch.Generator().manual_seed(seed)
+    ids = (torch.randperm(NB - 1, generator=g)[:n_pages] + 1).to(torch.int32)
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    cache = [torch.randn(2, NB, PS, H, D, generator=gd, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    return dict(L=L, H=H, D=D, PS=PS, NB=NB, T=T, n_pages=n_pages, ids=ids, names=layer_names(L),
+                cache=cache)
+
+
+def kvio_plan(w, meta_tokens=1024):
+    """The store/load pipeline's records over config4_inputs: 64 metas of 1024
+    tokens, each record = the 32 layers' page spans + the 4096-byte header."""
+    from daric_amd.kv_io import POSITION_SIZE
+    meta_pages = meta_tokens // w["PS"]
+    ids = w["ids"]
+    blocks = [(ids[m * meta_pages:(m + 1) * meta_pages].tolist(),) for m in range(w["n_pages"] // meta_pages)]
+    bpb = [2 * w["PS"] * w["H"] * w["D"] * 2] * w["L"]
+    rec = w["L"] * bpb[0] * meta_pages + POSITION_SIZE
+    return dict(blocks=blocks, bpb=bpb, rec=rec, offsets=[m * rec for m in range(len(blocks))])
+
+
 def run_config4(steps, warmup, seed=0):
     """KV offload/load: 65536 tokens (4096 pages) of a
     Llama-3-8B bf16 cache with a seeded random block table. Store: gather the
@@ -335,16 +374,10 @@ def run_config4(steps, warmup, seed=0):
     Load: the reverse (H2D, then scatter). Device-side and host-link rates are
     reported separately."""
     from daric_amd import cache_ops
-    c = CFG4
     dev = torch.device("cuda:0")
-    L, H, D, PS, NB = c["layers"], c["kv_heads"], c["head_dim"], c["block_size"], c["num_blocks"]
-    T = c["tokens"]
-    n_pages = T // PS
-    g = torch.Generator().manual_seed(seed)
-    ids = (torch.randperm(NB - 1, generator=g)[:n_pages] + 1).to(torch.int32)
-    names = layer_names(L)
-    gd = torch.Generator(device=dev).manual_seed(seed + 1)
-    cache = [torch.randn(2, NB, PS, H, D, generator=gd, device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    w = config4_inputs(dev, seed)
+    L, H, D, PS, T, n_pages = w["L"], w["H"], w["D"], w["PS"], w["T"], w["n_pages"]
+    ids, names, cache = w["ids"], w["names"], w["cache"]
     per_layer = 2 * n_pages * PS * H * D * 2
     staging = torch.empty(L * per_layer, dtype=torch.uint8, device=dev)
     host = torch.empty(L * per_layer, dtype=torch.uint8, pin_memory=True)
@@ -383,18 +416,15 @@ def run_config4(steps, warmup, seed=0):
     dev_bytes = 2 * L * per_layer
     link_bytes = L * per_layer
     # the store/load pipeline: 64 records of 1024 tokens, gather/scatter overlapped with host DMA
-    from daric_amd.kv_io import KVIOContext, POSITION_SIZE
+    from daric_amd.kv_io import KVIOContext
     del staging
     cp = None
     torch.cuda.empty_cache()
-    meta_pages = 1024 // PS
-    blocks = [(ids[m * meta_pages:(m + 1) * meta_pages].tolist(),) for m in range(n_pages // meta_pages)]
-    bpb = [2 * PS * H * D * 2] * L
-    rec = L * bpb[0] * meta_pages + POSITION_SIZE
+    plan = kvio_plan(w)
+    blocks, bpb, rec, rec_offs = plan["blocks"], plan["bpb"], plan["rec"], plan["offsets"]
     host_rec = torch.empty(len(blocks) * rec, dtype=torch.uint8, pin_memory=True)
     io = KVIOContext(names, [0] * L, bpb, [False] * L, dict(zip(names, cache)), host_rec,
                      staging_bytes=1 << 30)
-    rec_offs = [m * rec for m in range(len(blocks))]
 
     def timed(fn):
         torch.cuda.synchronize()
@@ -428,21 +458,19 @@ def run_config4(steps, warmup, seed=0):
                note="host link: pinned torch memory, one hipMemcpyAsync per layer record on a side "
                     "stream; pipelines: KVIOContext store/load of 64 records of 1024 tokens through "
                     "two 512 MiB staging halves (wall clock, host-synchronised)")
-    del cache, host
+    del w, cache, host
     torch.cuda.empty_cache()
     return out
 
 
-def run_config5(steps, warmup, seed=0):
-    """fp8 KV cache at Llama-3-70B per-layer KV shape: 80
-    layers x [2, 8193, 16, 8, 128] e4m3 with per-(layer, head) fp32 K scales
-    (amax / 448); 16 chunks x 2048 tokens staged as e4m3 codes of N(0,1)
-    values; one step = scatter_pages_rerotate (dequant -> rotate to offsets
-    0..32767 -> saturating RTNE requant -> scatter, 1280 jobs). The selection
-    at 10% per chunk (k = 205) on the fp8 cache is timed as a second figure."""
-    from daric_amd import cache_ops
+def config5_inputs(dev, seed=0):
+    """BASELINE config 5's inputs: fp8 KV cache at Llama-3-70B per-layer KV
+    shape, 80 layers x [2, 8193, 16, 8, 128] e4m3 (zeroed) with per-(layer,
+    head) fp32 K and V scales (amax / 448); 16 chunks x 2048 tokens staged in
+    the store's record layout as e4m3 codes of N(0,1) values at those scales;
+    the fused call's jobs (chunk c moves by 2048 c). Selection inputs: k = 205
+    of 2048 per chunk, recomputed K and V rows in bf16."""
     c = CFG5
-    dev = torch.device("cuda:0")
     L, H, D, PS, NB = c["layers"], c["kv_heads"], c["head_dim"], c["block_size"], c["num_blocks"]
     C, CT = c["chunks"], c["chunk_tokens"]
     T = C * CT
@@ -461,40 +489,82 @@ def run_config5(steps, warmup, seed=0):
         vals = torch.randn(n, generator=gd, device=dev) / 0.01      # codes of N(0,1) / (~4/448)
         staging[o:o + n] = vals.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
     del vals
-    cp = cache_ops.CacheCopier()
-    for l, (n, t) in enumerate(zip(names, cache)):
-        cp.register_layer(n, t, False)
-        cp.register_k_scale(n, k_scales[l].contiguous())
-    cp.register_store(staging)
-    jn, offs, sizes, flat, ioff, deltas, ntok = [], [], [], [], [0], [], []
+    jobs = dict(names=[], offsets=[], sizes=[], flat=[], ioff=[0], deltas=[], ntok=[])
     off = 0
     for ci in range(C):
         bids = ids[ci * (CT // PS):(ci + 1) * (CT // PS)].tolist()
         for n in names:
-            jn.append(n); offs.append(off); sizes.append(job_bytes); flat.extend(bids)
-            ioff.append(len(flat)); deltas.append(ci * CT); ntok.append(CT)
+            jobs["names"].append(n)
+            jobs["offsets"].append(off)
+            jobs["sizes"].append(job_bytes)
+            jobs["flat"].extend(bids)
+            jobs["ioff"].append(len(jobs["flat"]))
+            jobs["deltas"].append(ci * CT)
+            jobs["ntok"].append(CT)
             off += job_bytes
-    idx = torch.tensor(flat, dtype=torch.int32, device=dev)
+    idx = torch.tensor(jobs["flat"], dtype=torch.int32, device=dev)
     inv = (1.0 / (c["rope_theta"] ** (torch.arange(0, D, 2, dtype=torch.float32) / D))).to(dev)
-    stream = torch.cuda.current_stream(dev)
-    fused = time_steps(lambda: cp.scatter_pages_rerotate(jn, offs, sizes, idx, ioff, deltas, ntok, inv, D,
-                                                         True, stream.cuda_stream), steps, warmup, stream)
-    fused_bytes = T * L * 2 * (2 * H * D * 1)
-    # selection on the fp8 cache: recomputed K (bf16) vs the dequantised cached K
     k = max(1, int(round(c["k_frac"] * CT)))
-    bt = ids.to(dev)
-    chunks = [(ci * (CT // PS), ci * CT, CT, k) for ci in range(C)]
+    v_scales = (torch.rand(L, H, generator=gd, device=dev) * 2.0 + 3.0) / 448.0
     k_new = torch.randn(L, T, H, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    v_new = torch.randn(L, T, H, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    chunks = [(ci * (CT // PS), ci * CT, CT, k) for ci in range(C)]
+    return dict(L=L, H=H, D=D, PS=PS, NB=NB, C=C, CT=CT, T=T, ids=ids, names=names, cache=cache,
+                k_scales=k_scales, v_scales=v_scales, staging=staging, jobs=jobs, idx=idx, inv=inv,
+                job_bytes=job_bytes, k=k, bt=ids.to(dev), chunks=chunks, k_new=k_new, v_new=v_new)
+
+
+def run_config5(steps, warmup, seed=0):
+    """fp8 KV cache at Llama-3-70B per-layer KV shape (
+    config5_inputs): one step = scatter_pages_rerotate (dequant -> rotate to
+    offsets 0..32767 -> saturating RTNE requant -> scatter, 1280 jobs). The
+    selection at 10% per chunk (k = 205) on the fp8 cache -- deviation, top-k
+    and the quantising merge of the selected bf16 K/V rows -- is timed as a
+    second figure."""
+    from daric_amd import cache_ops
+    dev = torch.device("cuda:0")
+    w = config5_inputs(dev, seed)
+    L, H, D, C, T, k = w["L"], w["H"], w["D"], w["C"], w["T"], w["k"]
+    cache, k_scales, v_scales, j = w["cache"], w["k_scales"], w["v_scales"], w["jobs"]
+    cp = cache_ops.CacheCopier()
+    for l, (n, t) in enumerate(zip(w["names"], cache)):
+        cp.register_layer(n, t, False)
+        cp.register_k_scale(n, k_scales[l].contiguous())
+    cp.register_store(w["staging"])
+    stream = torch.cuda.current_stream(dev)
+    st = stream.cuda_stream
+    fused = time_steps(lambda: cp.scatter_pages_rerotate(j["names"], j["offsets"], j["sizes"], w["idx"],
+                                                         j["ioff"], j["deltas"], j["ntok"], w["inv"], D,
+                                                         True, st), steps, warmup, stream)
+    fused_bytes = T * L * 2 * (2 * H * D * 1)
+    # selection on the fp8 cache: recomputed K (bf16) vs the dequantised cached
+    # K, top-10%, then the selected bf16 K/V rows quantised into the cache
+    bt, chunks, k_new, v_new = w["bt"], w["chunks"], w["k_new"], w["v_new"]
     keys = torch.empty(L, T, dtype=torch.float32, device=dev)
     sel = torch.empty(L, C, k, dtype=torch.int32, device=dev)
 
+    def dev_step():
+        cache_ops.kv_deviation(cache, False, bt, k_new, chunks, keys=keys, stream=st, k_scales=k_scales)
+
+    def topk_step():
+        cache_ops.topk_per_chunk(keys, chunks, kmax=k, out=sel, stream=st)
+
+    def merge_step():
+        cache_ops.merge_rows(cache, False, bt, k_new, v_new, chunks, sel, stream=st, k_scales=k_scales,
+                             v_scales=v_scales)
+
     def sel_step():
-        cache_ops.kv_deviation(cache, False, bt, k_new, chunks, keys=keys, stream=stream.cuda_stream,
-                               k_scales=k_scales)
-        cache_ops.topk_per_chunk(keys, chunks, kmax=k, out=sel, stream=stream.cuda_stream)
+        dev_step()
+        topk_step()
+        merge_step()
 
     selection = time_steps(sel_step, steps, warmup, stream)
-    sel_bytes = T * L * H * D * (2 + 1) + 2 * T * L * 4 + C * L * k * 4
+    parts = {n: time_steps(f, steps, 1, stream)["kern_ms"]
+             for n, f in (("deviation", dev_step), ("topk", topk_step), ("merge", merge_step))}
+    dev_bytes = T * L * H * D * (2 + 1) + T * L * 4
+    topk_bytes = T * L * 4 + C * L * k * 4
+    merge_bytes = C * k * L * 2 * (H * D * (2 + 1))      # bf16 rows read, e4m3 codes written
+    sel_bytes = dev_bytes + topk_bytes + merge_bytes
     out = dict(workload="BASELINE config 5: fp8 e4m3 KV at Llama-3-70B per-layer shape, 80 layers, "
                         "16 chunks x 2048 tokens, dequant->rotate->requant+scatter to offsets 0..32767",
                tokens=T, ms_per_step=fused["step_ms"], tokens_per_s=T / (fused["step_ms"] / 1e3),
@@ -502,8 +572,13 @@ def run_config5(steps, warmup, seed=0):
                GBps=_gbps(fused_bytes, fused["kern_ms"]),
                frac=_gbps(fused_bytes, fused["kern_ms"]) / PEAK_HBM_GBPS,
                selection=dict(k=k, ms_per_step=selection["step_ms"], algorithmic_bytes=sel_bytes,
-                              GBps=_gbps(sel_bytes, selection["step_ms"])))
-    del cache, staging, cp, k_new, keys, sel
+                              GBps=_gbps(sel_bytes, selection["step_ms"]),
+                              kernels={"deviation": dict(ms=parts["deviation"], bytes=dev_bytes,
+                                                         GBps=_gbps(dev_bytes, parts["deviation"])),
+                                       "topk": dict(ms=parts["topk"], bytes=topk_bytes),
+                                       "merge_quantising": dict(ms=parts["merge"], bytes=merge_bytes,
+                                                                GBps=_gbps(merge_bytes, parts["merge"]))}))
+    del w, cache, cp, k_new, v_new, keys, sel
     torch.cuda.empty_cache()
     return out
 

@@ -352,19 +352,26 @@ def topk_per_chunk(keys: torch.Tensor, chunks, kmax: Optional[int] = None,
 
 def merge_rows(layers: Sequence[torch.Tensor], page_first: bool, block_table: torch.Tensor,
                k_new: torch.Tensor, v_new: Optional[torch.Tensor], chunks, sel_idx: torch.Tensor,
-               stream: int = 0) -> None:
-    """Write the selected recomputed K/V rows into their paged-cache slots."""
+               stream: int = 0, k_scales: Optional[torch.Tensor] = None,
+               v_scales: Optional[torch.Tensor] = None) -> None:
+    """Write the selected recomputed K/V rows into their paged-cache slots.
+    Rows in the cache's element type are copied; bf16/fp16 rows for an fp8
+    (e4m3) cache are quantised as sat_rtne(x / scale) with the [L, H] fp32
+    k_scales / v_scales (the fp8 write of vLLM's reshape_and_cache)."""
     layers = list(layers)
     dev = layers[0].device
     st = _resolve_stream(stream, dev)
     carr, n, _keep = _chunks(chunks)
     bt, kn, si = desc(block_table), desc(k_new), desc(sel_idx)
     vn = desc(v_new) if v_new is not None else None
+    ks = desc(k_scales) if k_scales is not None else None
+    vs = desc(v_scales) if v_scales is not None else None
     check(load().daric_merge_rows(_layer_array(layers), len(layers), 1 if page_first else 0,
                                   ctypes.byref(bt), ctypes.byref(kn),
                                   ctypes.byref(vn) if vn is not None else None, carr, n,
-                                  ctypes.byref(si), ctypes.c_uint64(st)))
-    _record(st, dev, block_table, k_new, v_new, sel_idx)
+                                  ctypes.byref(si), ctypes.byref(ks) if ks is not None else None,
+                                  ctypes.byref(vs) if vs is not None else None, ctypes.c_uint64(st)))
+    _record(st, dev, block_table, k_new, v_new, sel_idx, k_scales, v_scales)
 
 
 def timing_enable(enable: bool = True) -> None:

@@ -148,6 +148,8 @@ int elem_kind(const daric_tensor& t) {
     }
 }
 
+const char* quant_name(int kind) { return kind == kBF16 ? "bfloat16" : "float16"; }
+
 // Rotary layout resolution of reference adapter.py:311-368.
 struct RopeLayout {
     int64_t PS, H, D, sb, ss, sh, num_blocks, row_width;
@@ -1144,7 +1146,8 @@ int daric_topk_per_chunk(const daric_tensor* keys, const daric_chunk* chunks, in
 int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_first,
                      const daric_tensor* block_table, const daric_tensor* k_new,
                      const daric_tensor* v_new, const daric_chunk* chunks, int64_t n_chunks,
-                     const daric_tensor* sel_idx, uint64_t stream) {
+                     const daric_tensor* sel_idx, const daric_tensor* k_scales,
+                     const daric_tensor* v_scales, uint64_t stream) {
     return guarded([&] {
         DARIC_CHECK(n_layers > 0 && layers != nullptr, "layers must not be empty");
         for (int64_t i = 0; i < n_layers; ++i) check_tensor_struct(&layers[i], "kv layer");
@@ -1155,10 +1158,42 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
         check_block_table(block_table, t.device);
         int64_t T = 0, Tv = 0;
         check_rows_tensor(k_new, t, n_layers, g.H, g.D, "k_new", &T);
-        DARIC_CHECK(k_new->elem_size == t.elem_size, "k_new must have the cache's element size");
+        // Rows in the cache's element type are copied as bytes; bf16 / fp16
+        // rows for an fp8 (e4m3) cache are quantised with per-(layer, head)
+        // scales, as vLLM's fp8 cache write quantises them.
+        const int ck = elem_kind(t);
+        const int nk = elem_kind(*k_new);
+        const bool same_type = k_new->elem_size == t.elem_size &&
+                               (k_new->dtype == t.dtype || (ck == kE4M3 && nk == kE4M3));
+        const bool quant = ck == kE4M3 && (nk == kBF16 || nk == kF16);
+        DARIC_CHECK(same_type || quant,
+                    "k_new must have the cache's element type, or be bfloat16/float16 rows for an fp8 "
+                    "(e4m3) cache");
         if (g.v_off >= 0) {
             check_rows_tensor(v_new, t, n_layers, g.H, g.D, "v_new", &Tv);
-            DARIC_CHECK(Tv == T && v_new->elem_size == t.elem_size, "v_new must match k_new");
+            DARIC_CHECK(Tv == T && v_new->dtype == k_new->dtype && v_new->elem_size == k_new->elem_size,
+                        "v_new must match k_new");
+        }
+        const auto check_scales = [&](const daric_tensor* sc, const char* what) {
+            DARIC_CHECK(sc != nullptr && sc->data != nullptr, "merging ", quant_name(nk),
+                        " rows into an fp8 cache needs ", what);
+            check_tensor_struct(sc, what);
+            DARIC_CHECK(sc->device == t.device && sc->dtype == DARIC_DTYPE_FLOAT32 && is_contiguous(*sc) &&
+                        numel(*sc) == n_layers * g.H,
+                        what, " must be a contiguous float32 [n_layers, H] tensor on the layers' device");
+        };
+        if (quant) {
+            check_scales(k_scales, "k_scales");
+            if (g.v_off >= 0) check_scales(v_scales, "v_scales");
+            DARIC_CHECK(merge_fits_rows(g, t.elem_size, true),
+                        "quantising merge_rows needs head_dim % 8 == 0, 8-byte aligned cache rows and K+V "
+                        "rows of at most 32 KiB of recomputed values");
+            for (int64_t i = 0; i < n_layers; ++i)
+                DARIC_CHECK(aligned(layers[i].data, 8), "misaligned layer ", i);
+        } else {
+            DARIC_CHECK((k_scales == nullptr || k_scales->data == nullptr) &&
+                        (v_scales == nullptr || v_scales->data == nullptr),
+                        "k_scales / v_scales apply only when bf16/fp16 rows are merged into an fp8 cache");
         }
         check_tensor_struct(sel_idx, "sel_idx");
         DARIC_CHECK(sel_idx->device == t.device && sel_idx->dtype == DARIC_DTYPE_INT32 &&
@@ -1182,7 +1217,9 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
                      static_cast<const uint8_t*>(k_new->data),
                      g.v_off >= 0 ? static_cast<const uint8_t*>(v_new->data) : nullptr, T,
                      static_cast<int>(n_chunks), static_cast<const int32_t*>(sel_idx->data),
-                     static_cast<int>(kmax), st);
+                     static_cast<int>(kmax), quant ? nk : -1,
+                     quant ? static_cast<const float*>(k_scales->data) : nullptr,
+                     quant && g.v_off >= 0 ? static_cast<const float*>(v_scales->data) : nullptr, st);
     });
 }
 

@@ -128,9 +128,15 @@ void launch_deviation(const DescArg& d, int layer_off, int n_layers, const KVGeo
                       const float* k_scales, float* keys, hipStream_t stream);
 void launch_topk(const float* keys, int n_layers, int64_t T, const DescArg& d,
                  int n_chunks, int max_tokens, int32_t* out_idx, int kmax, hipStream_t stream);
+// merge: quant_from is -1 (rows are copied as bytes) or the ElemKind of
+// bf16 / fp16 rows quantised into an e4m3 cache with the [n_layers, H] fp32
+// k_scales / v_scales. merge_fits_rows: whether the row kernel takes the
+// geometry (required for quantising).
+bool merge_fits_rows(const KVGeom& g, int elem_size, bool quant);
 void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int elem_size,
                   const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,
-                  int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, hipStream_t stream);
+                  int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, int quant_from,
+                  const float* k_scales, const float* v_scales, hipStream_t stream);
 
 // Copies n16 16-byte units from host-pinned `src` to device `dst` on `stream`
 // (descriptor upload; both 16-byte aligned).

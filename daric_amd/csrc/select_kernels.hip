@@ -324,69 +324,107 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(
     }
 }
 
-// Row merge for 16-byte-aligned rows of at most 4 KiB: each wavefront moves
-// whole token rows -- the K and V rows of kRowTok selected tokens -- with one
-// selection / block-table lookup per token, all loads issued before the
-// stores. Measured on MI355X at configuration 3 (77 of 512 tokens per chunk,
-// 2 KiB rows) it ran ~7% faster than the per-unit merge_kernel.
-constexpr int kRowTok = 2;
-constexpr int kRowUnits = 4;   // 16-byte units per lane per row (rows <= 4 KiB)
+// Row merge for 16-byte-aligned rows. A workgroup writes `tpb` consecutive
+// selected slots of one (layer, chunk): its first lanes resolve each slot's
+// recomputed row and cache row (selection index, block table) into LDS; then
+// its lanes walk the 16-byte source units of those K and V rows, up to
+// kMergeUnits per lane, with every load issued before the first store. A lane
+// holds only its loaded values and recomputes the addresses from LDS at store
+// time (holding 16 destination pointers per lane took 112 VGPRs, capping the
+// kernel at 4 waves per SIMD).
+// MODE 0 copies bytes (rows and cache share their element type). MODE kBF16 /
+// kF16 + 1 quantises bf16 / fp16 rows into an e4m3 cache as vLLM's fp8 cache
+// write does: code = saturating RTNE of float32(x) / scale[l, h], the
+// division correctly rounded.
+constexpr int kMergeUnits = 8;
+constexpr int kMergeMaxTok = 64;
+constexpr int kMergeCopy = 0;
+constexpr int kMergeFromBF16 = kBF16 + 1;
+constexpr int kMergeFromF16 = kF16 + 1;
 
+template <int MODE>
 __global__ __launch_bounds__(kThreads) void merge_rows_kernel(
-    DescArg d, int layer_off, KVGeom g, int es, const int32_t* __restrict__ bt,
+    DescArg d, int layer_off, KVGeom g, int ces, const int32_t* __restrict__ bt,
     const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T,
-    int n_chunks, const int32_t* __restrict__ sel, int kmax, FastDiv d_upr) {
+    int n_chunks, const int32_t* __restrict__ sel, int kmax, int tpb, int units,
+    FastDiv d_tok_units, FastDiv d_upr, const float* __restrict__ k_scales,
+    const float* __restrict__ v_scales) {
+    __shared__ int64_t s_src[kMergeMaxTok];   // byte offset of the token's recomputed rows (-1: skip)
+    __shared__ int64_t s_dst[kMergeMaxTok];   // byte offset of the token's K row in the layer
     const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
     const int l = static_cast<int>(blockIdx.z);
     const int ci = static_cast<int>(blockIdx.y);
     const SelChunk c = desc_load(chunks + ci);
-    const int wave = static_cast<int>(threadIdx.x) >> 6;
-    const int lane = static_cast<int>(threadIdx.x) & 63;
-    const int q0 = (static_cast<int>(blockIdx.x) * kWaves + wave) * kRowTok;
-    const int32_t* srow = sel + (static_cast<int64_t>(l) * n_chunks + ci) * kmax;
-    uint8_t* __restrict__ base = layers[l];
-    const int upr = static_cast<int>(d_upr.d);     // 16-byte units per head row
-    const int units = g.H * upr;                   // per K (or V) token row
-    const int64_t rowbytes = static_cast<int64_t>(g.H) * g.D * es;
-    const int qmax = min(kmax, c.k);
-    u32x4 v[kRowTok][2][kRowUnits];
-    uint8_t* dst[kRowTok][2][kRowUnits];
-#pragma unroll
-    for (int t = 0; t < kRowTok; ++t) {
-        const int q = q0 + t;
-        int j = -1, blk = -1;
-        if (q < qmax) {
-            j = srow[q];
-            if (j >= 0 && j < c.n_tokens) blk = bt[c.bt_offset + j / g.PS];
-        }
-        const bool ok = blk > 0 && blk < g.num_blocks;
-#pragma unroll
-        for (int kv = 0; kv < 2; ++kv) {
-#pragma unroll
-            for (int r = 0; r < kRowUnits; ++r) {
-                dst[t][kv][r] = nullptr;
-                const int u = lane + r * 64;
-                if (!ok || u >= units || (kv == 1 && g.v_off < 0)) continue;
-                const int h = static_cast<int>(d_upr.div(static_cast<uint32_t>(u)));
-                const int un = u - h * upr;
-                const int64_t de = static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(j % g.PS) * g.ss +
-                                   static_cast<int64_t>(h) * g.sh + (kv ? g.v_off : 0);
-                const uint8_t* src = (kv ? v_new : k_new) +
-                                     (static_cast<int64_t>(l) * T + c.row_offset + j) * rowbytes +
-                                     static_cast<int64_t>(u) * 16;
-                dst[t][kv][r] = base + de * es + static_cast<int64_t>(un) * 16;
-                v[t][kv][r] = *reinterpret_cast<const u32x4*>(src);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int ses = MODE == kMergeCopy ? ces : 2;                    // source element size
+    const int64_t row_bytes = static_cast<int64_t>(g.H) * g.D * ses;
+    if (tid < tpb) {
+        const int q = static_cast<int>(blockIdx.x) * tpb + tid;
+        int64_t src = -1, dst = 0;
+        if (q < min(kmax, c.k)) {
+            const int j = sel[(static_cast<int64_t>(l) * n_chunks + ci) * kmax + q];
+            if (j >= 0 && j < c.n_tokens) {
+                const int blk = bt[c.bt_offset + j / g.PS];
+                if (blk > 0 && blk < g.num_blocks) {
+                    src = (static_cast<int64_t>(l) * T + c.row_offset + j) * row_bytes;
+                    dst = (static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(j % g.PS) * g.ss) * ces;
+                }
             }
         }
+        s_src[tid] = src;
+        s_dst[tid] = dst;
     }
+    __syncthreads();
+    const int tok_units = static_cast<int>(d_tok_units.d);   // units per token: K row, then V row
+    const int total = tpb * tok_units;
+    // Every slot loads (lanes past the end reload the last unit, skipped rows
+    // read the first unit of k_new) so that the values stay plain registers;
+    // only the stores are conditional.
+    u32x4 v[kMergeUnits];
 #pragma unroll
-    for (int t = 0; t < kRowTok; ++t)
+    for (int s = 0; s < kMergeUnits; ++s) {
+        const int f = min(tid + s * kThreads, total - 1);
+        const int t = static_cast<int>(d_tok_units.div(static_cast<uint32_t>(f)));
+        const int r = f - t * tok_units;
+        const int kv = r >= units ? 1 : 0;
+        const int64_t src = s_src[t];
+        const uint8_t* p = src >= 0 ? (kv ? v_new : k_new) + src + static_cast<int64_t>(r - kv * units) * 16 : k_new;
+        v[s] = *reinterpret_cast<const u32x4*>(p);
+    }
+    uint8_t* __restrict__ base = layers[l];
+    const int upr = static_cast<int>(d_upr.d);
+    // An opaque copy of the thread index: the compiler would otherwise keep
+    // every slot's decoded address alive across the loads (240 VGPRs).
+    int tid_s = tid;
+    asm volatile("" : "+v"(tid_s));
 #pragma unroll
-        for (int kv = 0; kv < 2; ++kv)
+    for (int s = 0; s < kMergeUnits; ++s) {
+        const int f = tid_s + s * kThreads;
+        if (f >= total) continue;
+        const int t = static_cast<int>(d_tok_units.div(static_cast<uint32_t>(f)));
+        const int r = f - t * tok_units;
+        const int kv = r >= units ? 1 : 0;
+        if (s_src[t] < 0) continue;
+        const int u = r - kv * units;
+        const int h = static_cast<int>(d_upr.div(static_cast<uint32_t>(u)));
+        const int un = u - h * upr;
+        uint8_t* dst = base + s_dst[t] + (static_cast<int64_t>(h) * g.sh + (kv ? g.v_off : 0)) * ces;
+        if constexpr (MODE == kMergeCopy) {
+            *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(un) * 16) = v[s];
+        } else {
+            const float sc = (kv ? v_scales : k_scales)[l * g.H + h];
+            float x[8];
 #pragma unroll
-            for (int r = 0; r < kRowUnits; ++r)
-                if (dst[t][kv][r] != nullptr) *reinterpret_cast<u32x4*>(dst[t][kv][r]) = v[t][kv][r];
+            for (int w = 0; w < 4; ++w) Elem<MODE - 1>::unpack_word(v[s][w], x + 2 * w);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = x[i] / sc;
+            u32x2 o;
+            o[0] = f32x4_to_e4m3_hw(x);
+            o[1] = f32x4_to_e4m3_hw(x + 4);
+            *reinterpret_cast<u32x2*>(dst + static_cast<int64_t>(un) * 8) = o;
+        }
+    }
 }
 
 }  // namespace
@@ -422,26 +460,51 @@ void launch_topk(const float* keys, int n_layers, int64_t T, const DescArg& d,
     check_launch("topk_per_chunk");
 }
 
+bool merge_fits_rows(const KVGeom& g, int elem_size, bool quant) {
+    const int ses = quant ? 2 : elem_size;
+    if ((g.D * ses) % 16 != 0) return false;
+    const int64_t dst_unit = quant ? 8 : 16;     // cache bytes per 16-byte source unit
+    if ((g.sb * elem_size) % dst_unit || (g.ss * elem_size) % dst_unit || (g.sh * elem_size) % dst_unit ||
+        (g.v_off >= 0 && (g.v_off * elem_size) % dst_unit))
+        return false;
+    const int64_t tok_units = static_cast<int64_t>(g.v_off >= 0 ? 2 : 1) * g.H * (g.D * ses / 16);
+    return tok_units <= static_cast<int64_t>(kThreads) * kMergeUnits;
+}
+
 void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int elem_size,
                   const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,
-                  int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>((kmax + kMergeTok - 1) / kMergeTok),
-                    static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
-    const bool vec = (g.D * elem_size) % 16 == 0 && (g.sb * elem_size) % 16 == 0 &&
-                     (g.ss * elem_size) % 16 == 0 && (g.sh * elem_size) % 16 == 0 &&
-                     (g.v_off < 0 || (g.v_off * elem_size) % 16 == 0);
-    const int upr = vec ? g.D * elem_size / 16 : 0;
-    if (vec && g.H * upr <= 64 * kRowUnits) {
-        const dim3 rgrid(static_cast<unsigned>((kmax + kWaves * kRowTok - 1) / (kWaves * kRowTok)),
-                         static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
-        DARIC_LAUNCH((merge_rows_kernel), rgrid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
-                     k_new, v_new, T, n_chunks, sel_idx, kmax, FastDiv(static_cast<uint32_t>(upr)));
-    } else if (vec)
-        DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table, k_new,
-                     v_new, T, n_chunks, sel_idx, kmax);
-    else
-        DARIC_LAUNCH((merge_kernel<1>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table, k_new,
-                     v_new, T, n_chunks, sel_idx, kmax);
+                  int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, int quant_from,
+                  const float* k_scales, const float* v_scales, hipStream_t stream) {
+    const bool quant = quant_from >= 0;
+    if (merge_fits_rows(g, elem_size, quant)) {
+        const int ses = quant ? 2 : elem_size;
+        const int upr = g.D * ses / 16;                              // source units per head row
+        const int units = g.H * upr;                                 // per K (or V) token row
+        const int tok_units = (g.v_off >= 0 ? 2 : 1) * units;
+        const int tpb = std::min(kMergeMaxTok, std::max(1, kThreads * kMergeUnits / tok_units));
+        const dim3 grid(static_cast<unsigned>((kmax + tpb - 1) / tpb), static_cast<unsigned>(n_chunks),
+                        static_cast<unsigned>(n_layers));
+        const FastDiv dtu(static_cast<uint32_t>(tok_units)), dupr(static_cast<uint32_t>(upr));
+#define DARIC_MR(M) DARIC_LAUNCH((merge_rows_kernel<M>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, \
+                                 block_table, k_new, v_new, T, n_chunks, sel_idx, kmax, tpb, units, dtu, dupr, \
+                                 k_scales, v_scales)
+        if (!quant) DARIC_MR(kMergeCopy);
+        else if (quant_from == kBF16) DARIC_MR(kMergeFromBF16);
+        else DARIC_MR(kMergeFromF16);
+#undef DARIC_MR
+    } else {
+        const dim3 grid(static_cast<unsigned>((kmax + kMergeTok - 1) / kMergeTok),
+                        static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
+        const bool vec = (g.D * elem_size) % 16 == 0 && (g.sb * elem_size) % 16 == 0 &&
+                         (g.ss * elem_size) % 16 == 0 && (g.sh * elem_size) % 16 == 0 &&
+                         (g.v_off < 0 || (g.v_off * elem_size) % 16 == 0);
+        if (vec)
+            DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
+                         k_new, v_new, T, n_chunks, sel_idx, kmax);
+        else
+            DARIC_LAUNCH((merge_kernel<1>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
+                         k_new, v_new, T, n_chunks, sel_idx, kmax);
+    }
     check_launch("merge_rows");
 }
 

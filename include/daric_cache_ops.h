@@ -302,13 +302,23 @@ int daric_topk_per_chunk(const daric_tensor* keys, const daric_chunk* chunks,
                          int64_t n_chunks, daric_tensor* out_idx, uint64_t stream);
 
 /* Write the selected rows of k_new / v_new ([n_layers, T, H, D]) into the K
- * and V rows of their slots in the paged caches. sel_idx is the output of
- * daric_topk_per_chunk (entries < 0 are ignored); slots in block 0 are
- * skipped like the reference's copy kernels skip block 0. */
+ * and V rows of their slots in the paged caches: the counterpart of the write
+ * vLLM's reshape_and_cache makes for the reference's recompute sub-requests
+ * (daric/integration/vllm/worker.py:336-345, utils.py:406-427). sel_idx is
+ * the output of daric_topk_per_chunk (entries < 0 are ignored); slots in
+ * block 0 are skipped like the reference's copy kernels skip block 0.
+ * Rows in the cache's element type are copied as bytes (k_scales and v_scales
+ * NULL). bfloat16 / float16 rows for an fp8 (e4m3) cache are quantised:
+ * code = saturating round-to-nearest-even e4m3 of float32(x) / scale, the
+ * division correctly rounded, with scale = k_scales[l, h] for K rows and
+ * v_scales[l, h] for V rows (contiguous [n_layers, H] fp32 device tensors of
+ * positive, finite values). */
 int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_first,
                      const daric_tensor* block_table, const daric_tensor* k_new,
                      const daric_tensor* v_new, const daric_chunk* chunks,
-                     int64_t n_chunks, const daric_tensor* sel_idx, uint64_t stream);
+                     int64_t n_chunks, const daric_tensor* sel_idx,
+                     const daric_tensor* k_scales, const daric_tensor* v_scales,
+                     uint64_t stream);
 
 #ifdef __cplusplus
 }

@@ -137,21 +137,52 @@ def topk_per_chunk(keys: np.ndarray, chunks, kmax: int) -> np.ndarray:
     return out
 
 
-def merge_rows(layers, page_first, block_table, k_new, v_new, chunks, sel_idx) -> None:
-    """Write selected K/V rows into their slots (block 0 / out of range skipped)."""
+def quantise_rows(rows: torch.Tensor, scales) -> torch.Tensor:
+    """bf16/fp16 rows [..., H, D] -> e4m3 codes (uint8) of float32(x) / scale[h],
+    the quotient correctly rounded to float32, then saturating RTNE. This is the
+    fp8 write of vLLM's reshape_and_cache for the recompute sub-requests'
+    rows (daric/integration/vllm/worker.py:336-345, utils.py:406-427)."""
+    x = rows.to(torch.float32).numpy()
+    s = np.asarray(scales, np.float32).reshape(-1, 1)
+    q = (x / s).astype(np.float32)
+    return torch.from_numpy(fp8.encode(q)).view(rows.shape)
+
+
+def merge_rows(layers, page_first, block_table, k_new, v_new, chunks, sel_idx,
+               k_scales=None, v_scales=None) -> None:
+    """Write selected K/V rows into their slots (block 0 / out of range skipped).
+    Rows in the cache's element type are copied; bf16/fp16 rows for an fp8
+    (uint8) cache are quantised with k_scales / v_scales [L, H]. The selected
+    slots of one call are distinct (as for the kernel, whose workgroups write
+    them concurrently)."""
+    quant = layers[0].dtype == torch.uint8 and k_new.dtype in (torch.bfloat16, torch.float16)
+    bt = np.asarray(block_table)
+    sel_idx = np.asarray(sel_idx)
     for l, layer in enumerate(layers):
         kv = k_rows_view(layer, page_first)
         vv = v_view(layer, page_first)
         nb, ps = kv.shape[0], kv.shape[1]
+        rows, blks, slots = [], [], []
         for c, (bt_offset, row_offset, n_tokens, _k) in enumerate(chunks):
-            for j in sel_idx[l, c]:
-                j = int(j)
-                if j < 0 or j >= n_tokens:
-                    continue
-                blk = int(np.asarray(block_table)[bt_offset + j // ps])
-                s = j % ps
-                if blk <= 0 or blk >= nb:
-                    continue
-                kv[blk, s].copy_(k_new[l, row_offset + j].view(kv.dtype))
-                if vv is not None:
-                    vv[blk, s].copy_(v_new[l, row_offset + j].view(vv.dtype))
+            j = sel_idx[l, c].astype(np.int64)
+            j = j[(j >= 0) & (j < n_tokens)]
+            blk = bt[bt_offset + j // ps].astype(np.int64)
+            keep = (blk > 0) & (blk < nb)
+            rows.append(row_offset + j[keep])
+            blks.append(blk[keep])
+            slots.append(j[keep] % ps)
+        if not rows:
+            continue
+        r = torch.from_numpy(np.concatenate(rows))
+        b = torch.from_numpy(np.concatenate(blks))
+        s = torch.from_numpy(np.concatenate(slots))
+        if r.numel() == 0:
+            continue
+        if quant:
+            kv[b, s] = quantise_rows(k_new[l, r], k_scales[l])
+            if vv is not None:
+                vv[b, s] = quantise_rows(v_new[l, r], v_scales[l])
+        else:
+            kv[b, s] = k_new[l, r].view(kv.dtype)
+            if vv is not None:
+                vv[b, s] = v_new[l, r].view(vv.dtype)

@@ -302,15 +302,25 @@ def test_selection_fuzz(dev, data):
     torch.cuda.synchronize()
     if kmax > 0:
         assert np.array_equal(sel_g.cpu().numpy(), sel_o)
-    # merge: recomputed rows in the cache's own element type
-    if dtype == torch.uint8:
+    # merge: recomputed rows in the cache's own element type, or (fp8 cache)
+    # bf16/fp16 rows quantised with per-(layer, head) K and V scales
+    quant = dtype == torch.uint8 and data.draw(st.booleans(), label="quantising merge")
+    ks = vs = None
+    if quant:
+        km = (torch.randn(L, T, H, D, generator=g) * 4).to(new_dtype)
+        vm = (torch.randn(L, T, H, D, generator=g) * 4).to(new_dtype)
+        ks = (0.002 + 0.02 * torch.rand(L, H, generator=g)).float()
+        vs = (0.002 + 0.02 * torch.rand(L, H, generator=g)).float()
+    elif dtype == torch.uint8:
         km = torch.from_numpy(ofp8.encode(torch.randn(L * T * H * D, generator=g).numpy())).view(L, T, H, D)
         vm = torch.from_numpy(ofp8.encode(torch.randn(L * T * H * D, generator=g).numpy())).view(L, T, H, D)
     else:
         km = torch.randn(L, T, H, D, generator=g).to(dtype)
         vm = torch.randn(L, T, H, D, generator=g).to(dtype)
-    osel.merge_rows(cpu, pf, bt, km, vm, chunks, sel_o)
-    cache_ops.merge_rows(gpu, pf, btd, km.to(dev), vm.to(dev), chunks, torch.from_numpy(sel_o).to(dev))
+    osel.merge_rows(cpu, pf, bt, km, vm, chunks, sel_o,
+                    k_scales=None if ks is None else ks.numpy(), v_scales=None if vs is None else vs.numpy())
+    cache_ops.merge_rows(gpu, pf, btd, km.to(dev), vm.to(dev), chunks, torch.from_numpy(sel_o).to(dev),
+                         k_scales=None if ks is None else ks.to(dev), v_scales=None if vs is None else vs.to(dev))
     torch.cuda.synchronize()
     for t, td in zip(cpu, gpu):
         assert same_bytes(td, t)

@@ -67,6 +67,60 @@ def test_deviation_topk_merge_parity(dev, layout):
         assert same_bytes(td, t)
 
 
+@pytest.mark.parametrize("layout", ["nhd", "hnd", "pf", "packed", "mla"])
+@pytest.mark.parametrize("row_dtype", [torch.bfloat16, torch.float16])
+def test_quantising_merge_parity(dev, layout, row_dtype):
+    """bf16/fp16 recomputed rows merged into an fp8 (e4m3) cache: codes of
+    x / scale[l, h] (K and V scales differ per layer and head), bit-exact
+    against the oracle; every other byte of the cache unchanged."""
+    layers, pf, bt, chunks, _k, _v = setup_case(dev, layout, dtype=torch.uint8, d=64, h=4, L=3)
+    cpu = [t for t, _ in layers]
+    gpu = [to_dev(t, dev) for t in cpu]
+    kv = osel.k_rows_view(cpu[0], pf)
+    L, H, D = len(cpu), kv.shape[2], kv.shape[3]
+    T = chunks[-1][1] + chunks[-1][2]
+    g = torch.Generator().manual_seed(21)
+    k_new = (torch.randn(L, T, H, D, generator=g) * 5).to(row_dtype)
+    v_new = (torch.randn(L, T, H, D, generator=g) * 5).to(row_dtype)
+    k_new[0, 0, 0, :4] = torch.tensor([1e4, -1e4, 0.0, -0.0])        # saturation and signed zero
+    ks = (0.004 + 0.03 * torch.rand(L, H, generator=g)).float()
+    vs = (0.004 + 0.03 * torch.rand(L, H, generator=g)).float()
+    kmax = max(c[3] for c in chunks)
+    sel = np.full((L, len(chunks), kmax), -1, np.int32)
+    rng = np.random.default_rng(5)
+    for l in range(L):
+        for c, (_bo, _ro, n, k) in enumerate(chunks):
+            sel[l, c, :k] = np.sort(rng.choice(n, size=k, replace=False))
+    sel[0, 0, 0] = 0
+    osel.merge_rows(cpu, pf, bt, k_new, v_new, chunks, sel, k_scales=ks.numpy(), v_scales=vs.numpy())
+    cache_ops.merge_rows(gpu, pf, torch.from_numpy(bt).to(dev), k_new.to(dev), v_new.to(dev), chunks,
+                         torch.from_numpy(sel).to(dev), k_scales=ks.to(dev), v_scales=vs.to(dev))
+    torch.cuda.synchronize()
+    for t, td in zip(cpu, gpu):
+        assert same_bytes(td, t)
+
+
+def test_quantising_merge_argument_errors(dev):
+    layers, pf, bt, chunks, _k, _v = setup_case(dev, "nhd", dtype=torch.uint8, L=1)
+    gpu = [to_dev(t, dev) for t, _ in layers]
+    T = chunks[-1][1] + chunks[-1][2]
+    k_new = torch.zeros(1, T, 4, 64, dtype=torch.bfloat16, device=dev)
+    sel = torch.zeros(1, len(chunks), 1, dtype=torch.int32, device=dev)
+    btd = torch.from_numpy(bt).to(dev)
+    sc = torch.ones(1, 4, device=dev)
+    with pytest.raises(RuntimeError, match="needs k_scales"):
+        cache_ops.merge_rows(gpu, pf, btd, k_new, k_new, chunks, sel)
+    with pytest.raises(RuntimeError, match="needs v_scales"):
+        cache_ops.merge_rows(gpu, pf, btd, k_new, k_new, chunks, sel, k_scales=sc)
+    with pytest.raises(RuntimeError, match="contiguous float32"):
+        cache_ops.merge_rows(gpu, pf, btd, k_new, k_new, chunks, sel, k_scales=sc[:, :2], v_scales=sc)
+    bf = [torch.zeros(2, 8, 16, 4, 64, dtype=torch.bfloat16, device=dev)]
+    with pytest.raises(RuntimeError, match="element type"):
+        cache_ops.merge_rows(bf, False, btd, k_new.half(), k_new.half(), chunks, sel)
+    with pytest.raises(RuntimeError, match="apply only"):
+        cache_ops.merge_rows(bf, False, btd, k_new, k_new, chunks, sel, k_scales=sc, v_scales=sc)
+
+
 def test_topk_ties_and_edge_k(dev):
     rng = np.random.default_rng(7)
     L, T = 2, 3000

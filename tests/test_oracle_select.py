@@ -132,3 +132,53 @@ def test_deviation_fp8_dequantises_with_per_head_scale():
         ref1 = ((kn - q) ** 2).sum()
         assert abs(keys[0, j] - ref) <= 1e-5 * ref
         assert abs(keys1[0, j] - ref1) <= 1e-5 * ref1
+
+
+def test_quantising_merge_is_pinned():
+    """bf16/fp16 rows merged into an fp8 cache: codes of x / scale[l, h].
+    Pinned by (1) scale 1 reducing to the e4m3 encoder, (2) power-of-two scales
+    scaling exactly, (3) an independent path -- float64 division rounded once
+    to float32 (which, for division, equals the correctly rounded float32
+    quotient) and torch's float8 cast after clamping -- with scales that differ
+    per head and between K and V, so a wrong head or K/V scale fails."""
+    from oracle import fp8
+    g = torch.Generator().manual_seed(9)
+    nb, ps, h, d, L, T = 7, 4, 3, 16, 2, 12
+    for dtype in (torch.bfloat16, torch.float16):
+        k_new = (torch.randn(L, T, h, d, generator=g) * 3).to(dtype)
+        v_new = (torch.randn(L, T, h, d, generator=g) * 3).to(dtype)
+        bt = np.array([3, 6, 1], np.int32)
+        chunks = [(0, 0, T, 5)]
+        sel = np.array([[[0, 2, 5, 9, 11]], [[1, 4, 6, 8, 10]]], np.int32)
+        for case in ("one", "pow2", "general"):
+            if case == "one":
+                ks = np.ones((L, h), np.float32)
+                vs = np.ones((L, h), np.float32)
+            elif case == "pow2":
+                ks = np.exp2(np.array([[-3, 0, 2], [1, -5, 4]], np.float32))
+                vs = np.exp2(np.array([[2, -1, 0], [-2, 3, -4]], np.float32))
+            else:
+                ks = np.array([[0.011, 0.0093, 0.0071], [0.013, 0.0088, 0.0102]], np.float32)
+                vs = np.array([[0.007, 0.0121, 0.0099], [0.0081, 0.0066, 0.0143]], np.float32)
+            layer = [torch.zeros(2, nb, ps, h, d, dtype=torch.uint8) for _ in range(L)]
+            select.merge_rows(layer, False, bt, k_new, v_new, chunks, sel, k_scales=ks, v_scales=vs)
+            for l in range(L):
+                for j in sel[l, 0]:
+                    blk, s = int(bt[j // ps]), int(j % ps)
+                    for kvi, (rows, sc) in enumerate(((k_new, ks), (v_new, vs))):
+                        got = layer[l][kvi, blk, s].numpy()
+                        x = rows[l, j].to(torch.float64)
+                        if case == "one":
+                            want = fp8.encode(rows[l, j].to(torch.float32).numpy())
+                        elif case == "pow2":
+                            want = fp8.encode((x * torch.from_numpy(1.0 / sc[l]).double()[:, None]).numpy())
+                        else:
+                            q = (x / torch.from_numpy(sc[l]).double()[:, None]).to(torch.float32)
+                            want = q.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+                        assert np.array_equal(got, want), (dtype, case, l, int(j), kvi)
+            # unselected slots stay zero
+            touched = {(int(bt[j // ps]), int(j % ps)) for l in range(L) for j in sel[l, 0]}
+            for b in range(nb):
+                for s in range(ps):
+                    if (b, s) not in touched:
+                        assert all(int(t[:, b, s].abs().sum()) == 0 for t in layer)
