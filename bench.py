@@ -54,13 +54,13 @@ def build_workload(cfg, device, num_blocks=None, layers=None, seed=0):
     g = torch.Generator().manual_seed(seed)
     ids = (torch.randperm(NB - 1, generator=g)[:n_pages] + 1).to(torch.int32)
     names = layer_names(L)
-    cache = [torch.empty(2, NB, PS, H, D, dtype=torch.bfloat16, device=device) for _ in range(L)]
+    dt = torch.float16 if cfg.get("dtype") == "fp16" else torch.bfloat16
+    cache = [torch.empty(2, NB, PS, H, D, dtype=dt, device=device) for _ in range(L)]
     span = PS * H * D * 2
     job_bytes = 2 * (CT // PS) * span
     gd = torch.Generator(device=device).manual_seed(seed + 1) if device.type == "cuda" else \
         torch.Generator().manual_seed(seed + 1)
-    staging = torch.randn(C * L * job_bytes // 2, generator=gd, device=device,
-                          dtype=torch.bfloat16).view(torch.uint8)
+    staging = torch.randn(C * L * job_bytes // 2, generator=gd, device=device, dtype=dt).view(torch.uint8)
     jobs = dict(names=[], offsets=[], sizes=[], flat=[], ioff=[0], deltas=[], ntok=[])
     off = 0
     for c in range(C):
@@ -79,10 +79,10 @@ def build_workload(cfg, device, num_blocks=None, layers=None, seed=0):
                 inv_freq=inv, span=span)
 
 
-def algorithmic_bytes(cfg, T=None, L=None):
+def algorithmic_bytes(cfg, T=None, L=None, e=2):
     L = L or cfg["layers"]
     T = T or cfg["chunks"] * cfg["chunk_tokens"]
-    return T * L * 2 * (2 * cfg["kv_heads"] * cfg["head_dim"] * 2)
+    return T * L * 2 * (2 * cfg["kv_heads"] * cfg["head_dim"] * e)
 
 
 def time_steps(step, steps, warmup, stream):
@@ -433,10 +433,44 @@ def run_config4(steps, warmup, seed=0):
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) * 1e3
 
-    timed(lambda: io.store(rec_offs, blocks, list(range(len(blocks)))))
-    store_ms = float(np.median([timed(lambda: io.store(rec_offs, blocks, list(range(len(blocks)))))
-                                for _ in range(n_host)]))
+    # every 1024-token record was saved at positions 0..1023; the fused load
+    # moves meta m to 1024 m (the request's concatenated offsets)
+    saved = [0] * len(blocks)
+    timed(lambda: io.store(rec_offs, blocks, saved))
+    store_ms = float(np.median([timed(lambda: io.store(rec_offs, blocks, saved)) for _ in range(n_host)]))
     load_ms = float(np.median([timed(lambda: io.load(rec_offs, blocks)) for _ in range(n_host)]))
+    inv = (1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))).to(dev)
+    rot = ([1024 * m for m in range(len(blocks))], [1024] * len(blocks), inv, D, True)
+    timed(lambda: io.load(rec_offs, blocks, rerotate=rot))
+    fused_ms = float(np.median([timed(lambda: io.load(rec_offs, blocks, rerotate=rot)) for _ in range(n_host)]))
+
+    def kernel_ms(fn):
+        """Average duration of the library's kernels launched by fn (dispatch events)."""
+        torch.cuda.synchronize()
+        cache_ops.timing_enable(True)
+        cache_ops.timing_read()
+        fn()
+        torch.cuda.synchronize()
+        ms, n = cache_ops.timing_read()
+        cache_ops.timing_enable(False)
+        return ms / max(n, 1), n
+
+    k_plain, n_plain = kernel_ms(lambda: io.load(rec_offs, blocks))
+    k_fused, n_fused = kernel_ms(lambda: io.load(rec_offs, blocks, rerotate=rot))
+    # the same fused calls with no host DMA running beside them: one staging
+    # half (4 records) re-scattered from device memory, as many times
+    from daric_amd.kv_io import build_copy_plan
+    flat, _, ioff, jn, jsz = build_copy_plan(names, [0] * L, bpb, [0] * 4, blocks[:4])
+    stg = np.cumsum([0] + jsz[:-1]).astype(np.int64).tolist()
+    idx4 = torch.from_numpy(flat).to(dev)
+    dl4 = [1024 * m for m in range(1, 5) for _ in range(L)]
+
+    def quiet():
+        for _ in range(n_fused):
+            io.read_copier.scatter_pages_rerotate(jn, stg, jsz, idx4, ioff, dl4, [1024] * len(jn), inv, D,
+                                                  True, stream.cuda_stream)
+
+    k_quiet, _ = kernel_ms(quiet)
     del io, host_rec
     out = dict(workload="BASELINE config 4: KV offload/load of 65536 tokens (4096 random pages), "
                         "Llama-3-8B KV shape bf16",
@@ -454,7 +488,16 @@ def run_config4(steps, warmup, seed=0):
                store_pipeline=dict(ms=store_ms, GBps=_gbps(link_bytes, store_ms),
                                    tokens_per_s=T / (store_ms / 1e3)),
                load_pipeline=dict(ms=load_ms, GBps=_gbps(link_bytes, load_ms),
-                                  tokens_per_s=T / (load_ms / 1e3)),
+                                  tokens_per_s=T / (load_ms / 1e3),
+                                  scatter_kernel_ms=k_plain, scatter_launches=n_plain),
+               load_pipeline_fused=dict(ms=fused_ms, GBps=_gbps(link_bytes, fused_ms),
+                                        tokens_per_s=T / (fused_ms / 1e3),
+                                        fused_kernel_ms=k_fused, fused_launches=n_fused,
+                                        fused_kernel_ms_without_dma=k_quiet,
+                                        note="KVIOContext.load(rerotate=...): each batch of 4 records "
+                                             "(128 jobs) scattered and re-rotated by 1024 m positions in "
+                                             "one scatter_pages_rerotate while the next batch's H2D runs; "
+                                             "fused_kernel_ms_without_dma: the same 128-job call alone"),
                note="host link: pinned torch memory, one hipMemcpyAsync per layer record on a side "
                     "stream; pipelines: KVIOContext store/load of 64 records of 1024 tokens through "
                     "two 512 MiB staging halves (wall clock, host-synchronised)")
@@ -583,59 +626,94 @@ def run_config5(steps, warmup, seed=0):
     return out
 
 
-def cpu_threads() -> int:
-    """Host threads for the CPU baseline: the cores this process may run on,
-    at most 16 (one GPU's share of the box)."""
+CFG1 = dict(layers=16, kv_heads=8, head_dim=64, block_size=16, num_blocks=1024, chunks=4, chunk_tokens=512,
+            rope_theta=500000.0, dtype="fp16")
+
+
+def host_cpu() -> dict:
+    """The host's CPU: model name, the cores this process may run on, and the
+    threads the baseline uses (at most 16, one GPU's share of an MI355X box)."""
     try:
-        n = len(os.sched_getaffinity(0))
+        avail = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        avail = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(cpu_model=model, cores_available=avail, threads=max(1, min(16, avail)),
+                thread_cap="16: one GPU's share of the box's cores")
+
+
+def cpu_threads() -> int:
+    return host_cpu()["threads"]
+
+
+def _time_cpu(run, budget_s, min_runs=5, max_runs=20):
+    """One warm-up, then at least min_runs timed runs (more while the budget
+    lasts, at most max_runs); returns (median seconds, runs)."""
+    run()
+    times = []
+    while len(times) < max_runs and (len(times) < min_runs or sum(times) < budget_s):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
 
 
 def run_cpu_baseline(cfg, budget_s=12.0):
-    """The CPU oracle's fused scatter + re-rotate over the whole workload (all
-    layers, 256 jobs) with a reduced 1024-block pool (same bytes moved): one
-    warm-up run, then repeated runs until `budget_s` has elapsed (at most 20);
-    the median run time gives tokens/s. It runs the oracle's C restatement
-    (oracle/c/oracle_copy.c) on cpu_threads() OpenMP threads, or the numpy
-    oracle on one thread when the C library has not been built."""
+    """The CPU oracle's fused scatter + re-rotate, timed on this host: the C
+    restatement (oracle/c/oracle_copy.c) on host_cpu()["threads"] OpenMP
+    threads, or the numpy oracle on one thread when the C library has not been
+    built. Two workloads: the headline's (config 2: all 32 layers, 256 jobs,
+    with a reduced 1024-block pool -- the same bytes move) and BASELINE
+    config 1 at its real size (16 layers of [2, 1024, 16, 8, 64] fp16, 4
+    chunks of 512 tokens moved to 0, 512, 1024, 1536). Median of at least 5
+    runs after one warm-up each."""
     from oracle import native
     from oracle.copy import OracleCopier
-    threads = cpu_threads()
+    cpu = host_cpu()
+    threads = cpu["threads"]
     if native.available():
-        oc = native.NativeOracleCopier(threads)
+        make = lambda: native.NativeOracleCopier(threads)
         what = f"the C restatement oracle/c/oracle_copy.c on {threads} OpenMP threads"
     else:
         torch.set_num_threads(1)
         threads = 1
-        oc = OracleCopier()
+        make = OracleCopier
         what = "the numpy oracle oracle/copy.py on one thread"
-    w = build_workload(cfg, torch.device("cpu"), num_blocks=1024)
-    j = w["jobs"]
-    inv = w["inv_freq"].numpy()
-    for name, t in zip(w["names"], w["cache"]):
-        oc.register_layer(name, t, False)
-    oc.register_store(w["staging"])
-    idx = torch.tensor(j["flat"], dtype=torch.int32)
 
-    def run():
-        oc.scatter_pages_rerotate(j["names"], j["offsets"], j["sizes"], idx, j["ioff"], j["deltas"],
-                                  j["ntok"], inv, cfg["head_dim"], True)
+    def timed(c, pool, budget):
+        oc = make()
+        w = build_workload(c, torch.device("cpu"), num_blocks=pool)
+        j = w["jobs"]
+        inv = w["inv_freq"].numpy()
+        for name, t in zip(w["names"], w["cache"]):
+            oc.register_layer(name, t, False)
+        oc.register_store(w["staging"])
+        idx = torch.tensor(j["flat"], dtype=torch.int32)
+        med, n = _time_cpu(lambda: oc.scatter_pages_rerotate(j["names"], j["offsets"], j["sizes"], idx,
+                                                             j["ioff"], j["deltas"], j["ntok"], inv,
+                                                             c["head_dim"], True), budget)
+        return w["T"], med, n
 
-    run()
-    times = []
-    while len(times) < 20 and sum(times) < budget_s:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    T = w["T"]
+    T, med, n = timed(cfg, 1024, budget_s)
+    T1, med1, n1 = timed(CFG1, CFG1["num_blocks"], budget_s / 4)
     return dict(value=T / med, unit="reused KV tokens/s", cores=threads, kind="port",
-                sample=f"whole workload (32 layers x 8 chunks x 1024 tokens, 1024-block pool) through "
-                       f"scatter_pages_rerotate of {what}, median of {len(times)} runs "
-                       f"({med:.3f} s each) after one warm-up",
-                GBps=algorithmic_bytes(cfg) / med / 1e9)
+                sample=f"whole config-2 workload (32 layers x 8 chunks x 1024 tokens, 1024-block pool) "
+                       f"through scatter_pages_rerotate of {what}, median of {n} runs ({med:.3f} s each) "
+                       f"after one warm-up",
+                GBps=algorithmic_bytes(cfg) / med / 1e9,
+                cores_available=cpu["cores_available"], thread_cap=cpu["thread_cap"],
+                cpu_model=cpu["cpu_model"], torch_version=torch.__version__,
+                config1=dict(value=T1 / med1, unit="reused KV tokens/s",
+                             GBps=algorithmic_bytes(CFG1, e=2) / med1 / 1e9, seconds=med1, runs=n1,
+                             workload="BASELINE config 1 at its real size: 16 layers x [2, 1024, 16, 8, 64] "
+                                      "fp16, 4 x 512 tokens scattered and moved to 0/512/1024/1536"))
 
 
 def run_copy_calibration(steps, nbytes=1 << 30):
@@ -733,7 +811,7 @@ def main():
                              "note": "rerotate_pages of chunks 1..7 (chunk 0 does not move) in all "
                                      "layers: K rotated elements read and written"},
         "extra": extra,
-        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "GBps")},
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line))
 

@@ -319,9 +319,16 @@ def kv_deviation(layers: Sequence[torch.Tensor], page_first: bool, block_table: 
     cache (None: scale 1)."""
     layers = list(layers)
     dev = layers[0].device
-    if keys is None:
-        keys = torch.zeros(len(layers), k_new.shape[1], dtype=torch.float32, device=dev)
     st = _resolve_stream(stream, dev)
+    if keys is None:
+        # zeroed on the launch stream: rows outside every chunk stay 0, and the
+        # fill is ordered before the kernel whatever stream the caller passed
+        shape = (len(layers), k_new.shape[1])
+        if st == _resolve_stream(0, dev):
+            keys = torch.zeros(shape, dtype=torch.float32, device=dev)
+        else:
+            with torch.cuda.stream(_ext_stream(st, dev)):
+                keys = torch.zeros(shape, dtype=torch.float32, device=dev)
     carr, n, _keep = _chunks(chunks)
     bt, kn, kd = desc(block_table), desc(k_new), desc(keys)
     ks = desc(k_scales) if k_scales is not None else None

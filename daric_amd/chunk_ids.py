@@ -1,29 +1,31 @@
-"""Chunk ids of reused prompt segments: the reuse controller's hash chain
-(reference daric/utils/common.py:8-26, daric/reuse_controller/searcher.py:39-188),
-on the host.
+"""Chunk ids of reused prompt segments, on the host: the ids under which the
+reuse controller stores and finds KV records (reference
+daric/utils/common.py:8-26 for the hash input, daric/reuse_controller/
+searcher.py:39-188 for the pieces and the chain).
 
-A prompt is cut at its group boundaries ind_ptr; inside each group, pieces of
-max_chunk_len tokens are cached, and the last group's tail that does not fill
-a whole piece is not (it is recomputed). Each piece's id is
-xxh64(parent_id_bytes || tokens as little-endian uint32), hex-encoded:
+Format. A prompt is cut at its group boundaries ind_ptr. Each non-empty group
+is cut into pieces of max_chunk_len tokens (the last piece of a group may be
+shorter), except that the final group keeps only whole pieces: its tail is
+recomputed, never cached. A piece's id is the lowercase hex XXH64 (seed 0) of
 
-  - prefix mode: the parent of every piece is the previous piece (the first
-    piece's parent is the system prefix "<model>_<tp>_<pp>"), so an id names
-    the whole prefix up to its piece;
-  - independent mode: the chain restarts from the system prefix at every
-    group boundary, so a group's pieces are reusable at any position
-    (position-independent caching; the K rows are re-rotated on reuse).
+    parent_id (UTF-8)  ||  the piece's token ids as little-endian uint32
 
-These ids key the store records that the store/load path moves
-(daric_amd.kv_io); the hashing is byte work on a few KiB per request and stays
-on the CPU, where the token ids are.
+where the parent is the previous piece's id, or the system prefix
+"<model>_<tp>_<pp>" for the first piece of a chain. In prefix mode one chain
+runs through the whole prompt, so an id names everything before it; in
+independent mode the chain restarts at every group, so a group's pieces get
+the same ids wherever the group sits (position-independent caching; the K
+rows are re-rotated on reuse).
+
+These ids key the records that the store/load path moves (daric_amd.kv_io);
+the hashing is a few KiB of byte work per request and stays on the CPU, where
+the token ids are.
 """
 from __future__ import annotations
 
-import sys
-from array import array
 from typing import List, Optional, Sequence, Tuple, Union
 
+import numpy as np
 import xxhash
 
 __all__ = ["token_ids_to_bytes", "get_hash_id", "split_chunk_ptr", "prefix_chunk_ids",
@@ -31,75 +33,67 @@ __all__ = ["token_ids_to_bytes", "get_hash_id", "split_chunk_ptr", "prefix_chunk
 
 
 def token_ids_to_bytes(token_ids: Sequence[int]) -> bytes:
-    """Token ids as consecutive little-endian uint32 (common.py:8-14)."""
-    arr = array("I", token_ids)
-    if arr.itemsize != 4:
-        raise RuntimeError(f"Unexpected unsigned int size: {arr.itemsize}")
-    if sys.byteorder != "little":
-        arr.byteswap()
-    return arr.tobytes()
+    """Token ids as consecutive little-endian uint32 words; ids outside
+    [0, 2^32) raise OverflowError."""
+    return np.asarray(token_ids, dtype="<u4").tobytes()
 
 
 def get_hash_id(hash_input: bytes, prefix: Optional[bytes] = None,
                 type: str = "str") -> Union[str, int]:
-    """xxh64 (seed 0) of prefix || hash_input; hex string, or int for type="int"
-    (common.py:16-26)."""
-    h = xxhash.xxh64()
-    if prefix is not None:
-        h.update(prefix)
-    h.update(hash_input)
-    return h.intdigest() if type == "int" else h.hexdigest()
+    """XXH64 (seed 0) of prefix || hash_input: lowercase hex, or the integer
+    for type="int"."""
+    data = hash_input if prefix is None else bytes(prefix) + bytes(hash_input)
+    return xxhash.xxh64_intdigest(data) if type == "int" else xxhash.xxh64_hexdigest(data)
 
 
 def split_chunk_ptr(ind_ptr: Sequence[int], max_chunk_len: int) -> Tuple[List[int], List[int]]:
-    """Piece boundaries (searcher.py:39-59): every non-empty group is cut into
-    pieces of at most max_chunk_len tokens, laid end to end from 0; the last
-    group keeps only whole pieces. Returns (piece boundaries, group boundaries)."""
-    bounds = [0]
-    last = len(ind_ptr) - 2
-    for i in range(len(ind_ptr) - 1):
-        length = ind_ptr[i + 1] - ind_ptr[i]
-        if length <= 0:
-            continue
-        keep = length - (length % max_chunk_len if i == last else 0)
-        done = 0
-        while done < keep:
-            step = min(max_chunk_len, keep - done)
-            bounds.append(bounds[-1] + step)
-            done += step
-    return bounds, list(ind_ptr)
+    """(piece boundaries, group boundaries). Piece lengths: each non-empty
+    group's cached length split into max_chunk_len-token pieces, the final
+    group's cached length rounded down to a multiple of max_chunk_len."""
+    ptr = np.asarray(ind_ptr, dtype=np.int64)
+    m = int(max_chunk_len)
+    lengths = np.maximum(np.diff(ptr), 0)
+    if lengths.size:
+        lengths[-1] -= lengths[-1] % m
+    pieces = -(-lengths // m)                        # pieces per group
+    # every piece is max_chunk_len long except each group's last one
+    piece_len = np.full(int(pieces.sum()), m, dtype=np.int64)
+    ends = np.cumsum(pieces) - 1
+    has = pieces > 0
+    piece_len[ends[has]] = lengths[has] - (pieces[has] - 1) * m
+    bounds = np.concatenate([[0], np.cumsum(piece_len)])
+    return bounds.tolist(), list(ind_ptr)
+
+
+def _chain(tokens, bounds, restart, system_prefix: str) -> List[Tuple[str, List[int]]]:
+    toks = np.asarray(tokens, dtype="<u4")
+    out = []
+    parent = system_prefix
+    for a, b, fresh in zip(bounds[:-1], bounds[1:], restart):
+        if fresh:
+            parent = system_prefix
+        cid = xxhash.xxh64_hexdigest(parent.encode() + toks[a:b].tobytes())
+        out.append((cid, [a, b]))
+        parent = cid
+    return out
 
 
 def prefix_chunk_ids(tokens: Sequence[int], ind_ptr: Sequence[int], max_chunk_len: int,
                      system_prefix: str) -> List[Tuple[str, List[int]]]:
-    """(id, [start, end)) of every piece, each chained on its predecessor
-    (PrefixSearcher.search, searcher.py:79-93)."""
+    """(id, [start, end)) of every piece, one chain through the whole prompt
+    (the reference's PrefixSearcher, searcher.py:79-93)."""
     bounds, _ = split_chunk_ptr(ind_ptr, max_chunk_len)
-    out = []
-    parent = system_prefix
-    for a, b in zip(bounds, bounds[1:]):
-        cid = get_hash_id(token_ids_to_bytes(tokens[a:b]), prefix=parent.encode())
-        out.append((cid, [a, b]))
-        parent = cid
-    return out
+    return _chain(tokens, bounds, [False] * (len(bounds) - 1), system_prefix)
 
 
 def independent_chunk_ids(tokens: Sequence[int], ind_ptr: Sequence[int], max_chunk_len: int,
                           system_prefix: str) -> List[Tuple[str, List[int]]]:
-    """(id, [start, end)) of every piece, the chain restarting from the system
-    prefix in each group (IndependentSearcher.search, searcher.py:133-149)."""
+    """(id, [start, end)) of every piece, the chain restarting at every group
+    (the reference's IndependentSearcher, searcher.py:133-149)."""
     if len(tokens) != ind_ptr[-1]:
-        raise AssertionError(f"Length mismatch between prompt_token_ids {len(tokens)} "
-                             f"and ind_ptr {ind_ptr[-1]}")
+        raise ValueError(f"the prompt has {len(tokens)} tokens but its group boundaries end at {ind_ptr[-1]}")
     bounds, groups = split_chunk_ptr(ind_ptr, max_chunk_len)
-    out = []
-    g = 0
-    parent = system_prefix
-    for a, b in zip(bounds, bounds[1:]):
-        while a >= groups[g + 1]:
-            g += 1
-            parent = system_prefix
-        cid = get_hash_id(token_ids_to_bytes(tokens[a:b]), prefix=parent.encode())
-        out.append((cid, [a, b]))
-        parent = cid
-    return out
+    starts = np.asarray(bounds[:-1], dtype=np.int64)
+    group_of = np.searchsorted(np.asarray(groups, dtype=np.int64), starts, side="right") - 1
+    restart = np.concatenate([[True], group_of[1:] != group_of[:-1]]) if starts.size else []
+    return _chain(tokens, bounds, restart, system_prefix)

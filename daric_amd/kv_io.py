@@ -21,13 +21,18 @@ half.
 
 Store and load have separate staging buffers and streams, as the reference's
 staging and read_staging (gpu_kv_io.py:150-151), so one thread may store while
-another loads. Two stores, or two loads, must not run at once on one context.
+another loads. Two stores (or two loads) on one context take turns: each
+direction has a lock, where the reference lets concurrent calls share one
+staging buffer. close() drains the context as the reference's
+RankIPCContext.close does (gpu_kv_io.py:157-205).
 
 The host buffer must be page-locked memory (torch pin_memory or hipHostMalloc)
 so the DMA engines can reach it.
 """
 from __future__ import annotations
 
+import threading
+from contextlib import contextmanager
 from typing import List, Optional, Sequence
 
 import numpy as np
@@ -45,26 +50,29 @@ DEFAULT_STAGING_BYTES = 256 << 20
 
 
 def split_registration_copies(stg_offsets, shm_offsets, sizes, chunk_bytes=REGISTRATION_CHUNK_BYTES):
-    """Cuts each (staging, host, size) region where the host offset crosses a
-    multiple of chunk_bytes (the reference registers host memory in 1 GiB
-    pieces and never lets one copy span two, gpu_kv_io.py:110-127)."""
-    if not (len(stg_offsets) == len(shm_offsets) == len(sizes)):
-        raise ValueError("Copy offsets and sizes must have the same length.")
+    """(staging offsets, host offsets, sizes) of the copies, each region cut
+    where its host range crosses a multiple of chunk_bytes: the reference
+    registers host memory in 1 GiB pieces and no copy may span two of them
+    (gpu_kv_io.py:110-127). Region r touches registration chunks
+    host[r] // chunk .. (host[r] + size[r] - 1) // chunk; its k-th piece is its
+    intersection with the k-th of them. Empty regions give no copy."""
+    stg = np.asarray(stg_offsets, dtype=np.int64).reshape(-1)
+    host = np.asarray(shm_offsets, dtype=np.int64).reshape(-1)
+    size = np.asarray(sizes, dtype=np.int64).reshape(-1)
+    if not stg.size == host.size == size.size:
+        raise ValueError(f"{stg.size} staging offsets, {host.size} host offsets and {size.size} sizes: "
+                         "one of each per region is needed")
     if chunk_bytes <= 0:
-        raise ValueError("Registration chunk size must be positive.")
-    rs, rh, rn = [], [], []
-    for s, h, n in zip(stg_offsets, shm_offsets, sizes):
-        if s < 0 or h < 0 or n < 0:
-            raise ValueError("Copy offsets and sizes must be non-negative.")
-        while n > 0:
-            take = min(n, chunk_bytes - h % chunk_bytes)
-            rs.append(s)
-            rh.append(h)
-            rn.append(take)
-            s += take
-            h += take
-            n -= take
-    return rs, rh, rn
+        raise ValueError(f"chunk_bytes must be positive, got {chunk_bytes}")
+    if (stg < 0).any() or (host < 0).any() or (size < 0).any():
+        raise ValueError("staging offsets, host offsets and sizes must be non-negative")
+    first = host // chunk_bytes
+    pieces = np.where(size > 0, (host + size - 1) // chunk_bytes - first + 1, 0)
+    region = np.repeat(np.arange(size.size), pieces)
+    k = np.arange(region.size) - np.repeat(np.cumsum(pieces) - pieces, pieces)
+    lo = np.maximum(host[region], (first[region] + k) * chunk_bytes)
+    hi = np.minimum(host[region] + size[region], (first[region] + k + 1) * chunk_bytes)
+    return (stg[region] + (lo - host[region])).tolist(), lo.tolist(), (hi - lo).tolist()
 
 
 def per_meta_cache_size(layer_names, group_idxs, layer_bpbs, block_ids_list, layer_name=None):
@@ -150,6 +158,62 @@ class KVIOContext:
         self.write_copier.register_store(self._store.staging)
         self.read_copier.register_store(self._load.staging)
         self.done = None   # after load(): event marking the end of its device work
+        self._lifecycle = threading.Condition()
+        self._inflight = 0
+        self._closed = False
+        self._store_lock = threading.Lock()
+        self._load_lock = threading.Lock()
+
+    # ------------------------------------------------------------ lifecycle
+    @property
+    def closed(self) -> bool:
+        return self._closed
+
+    @contextmanager
+    def _operation(self, lock: threading.Lock):
+        with self._lifecycle:
+            if self._closed:
+                raise RuntimeError("KV IO: context is closed")
+            self._inflight += 1
+        try:
+            with lock:
+                yield
+        finally:
+            with self._lifecycle:
+                self._inflight -= 1
+                if self._inflight == 0:
+                    self._lifecycle.notify_all()
+
+    def close(self) -> None:
+        """Refuses further stores and loads, waits for the running ones and
+        for their queued device work, then drops the copiers and staging
+        buffers (the reference's RankIPCContext.close, gpu_kv_io.py:182-205).
+        Calling it again does nothing."""
+        with self._lifecycle:
+            self._closed = True
+            while self._inflight > 0:
+                self._lifecycle.wait()
+            pipes = [p for p in (self._store, self._load) if p is not None]
+            self._store = self._load = None
+        for pipe in pipes:
+            pipe.kernels.synchronize()
+            pipe.dma.synchronize()
+        self.write_copier = None
+        self.read_copier = None
+
+    def _upload_indices(self, flats, stream) -> List[torch.Tensor]:
+        """Block ids of every batch of a call in one pinned, non-blocking copy
+        on `stream`, issued before the call's waits, so the host never blocks
+        on a batch's DMA to upload the next batch's ids."""
+        sizes = [len(f) for f in flats]
+        host = torch.from_numpy(np.concatenate(flats) if flats else np.zeros(0, np.int32)).pin_memory()
+        with torch.cuda.stream(stream):
+            dev = host.to(self.device, non_blocking=True)
+        out, o = [], 0
+        for n in sizes:
+            out.append(dev[o:o + n])
+            o += n
+        return out
 
     # ------------------------------------------------------------ helpers
     def cache_sizes(self, block_ids_list, layer_name=None) -> List[int]:
@@ -189,24 +253,26 @@ class KVIOContext:
         """Writes one record per meta at host offset offsets[i] (the reference's
         _do_store after allocation). Returns once the records, headers included,
         are in host memory."""
+        with self._operation(self._store_lock):
+            self._store_records(offsets, block_ids_list, saved_positions, layer_name, wait_stream)
+
+    def _store_records(self, offsets, block_ids_list, saved_positions, layer_name, wait_stream):
         offsets = [int(o) for o in offsets]
         sizes = self.cache_sizes(block_ids_list, layer_name)
         pipe = self._store
+        per_meta = 1 if layer_name is not None else len(self.layer_names)
+        plans = [(i, j, build_copy_plan(self.layer_names, self.group_idxs, self.layer_bpbs, offsets[i:j],
+                                        block_ids_list[i:j], layer_name))
+                 for i, j in self._batches(sizes, self.half, self.MAX_BATCH_SIZE)]
+        idxs = self._upload_indices([p[2][0] for p in plans], pipe.kernels)
         if wait_stream is not None:
             pipe.kernels.wait_stream(wait_stream)
-        per_meta = 1 if layer_name is not None else len(self.layer_names)
-        b = 0
-        for i, j in self._batches(sizes, self.half, self.MAX_BATCH_SIZE):
+        for b, ((i, j, (flat, host_off, ioff, names, job_sz)), idx) in enumerate(zip(plans, idxs)):
             h = b % 2
             base = h * self.half
-            flat, host_off, ioff, names, job_sz = build_copy_plan(
-                self.layer_names, self.group_idxs, self.layer_bpbs, offsets[i:j],
-                block_ids_list[i:j], layer_name)
             stg = np.cumsum([0] + job_sz[:-1]).astype(np.int64) + base
             if pipe.half_free[h] is not None:
                 pipe.kernels.wait_event(pipe.half_free[h])
-            with torch.cuda.stream(pipe.kernels):
-                idx = torch.from_numpy(flat).to(self.device, non_blocking=False)
             self.write_copier.gather_pages(names, stg.tolist(), job_sz, idx, ioff,
                                            pipe.kernels.cuda_stream)
             gathered = torch.cuda.Event()
@@ -218,7 +284,6 @@ class KVIOContext:
             ev = torch.cuda.Event()
             ev.record(pipe.dma)
             pipe.half_free[h] = ev
-            b += 1
         pipe.dma.synchronize()
         self._write_positions([o + s for o, s in zip(offsets, sizes)], saved_positions)
 
@@ -234,20 +299,24 @@ class KVIOContext:
         first, which live in host memory. Device work is left queued on the
         load's kernel stream; self.done, an event recorded after it, marks its
         end."""
+        with self._operation(self._load_lock):
+            return self._load_records(offsets, block_ids_list, layer_name, wait_stream, rerotate)
+
+    def _load_records(self, offsets, block_ids_list, layer_name, wait_stream, rerotate):
         offsets = [int(o) for o in offsets]
         sizes = self.cache_sizes(block_ids_list, layer_name)
         saved = self.read_positions([o + s for o, s in zip(offsets, sizes)])
         pipe = self._load
+        per_meta = 1 if layer_name is not None else len(self.layer_names)
+        plans = [(i, j, build_copy_plan(self.layer_names, self.group_idxs, self.layer_bpbs, offsets[i:j],
+                                        block_ids_list[i:j], layer_name))
+                 for i, j in self._batches(sizes, self.half, 1 << 30)]
+        idxs = self._upload_indices([p[2][0] for p in plans], pipe.kernels)
         if wait_stream is not None:
             pipe.dma.wait_stream(wait_stream)
-        per_meta = 1 if layer_name is not None else len(self.layer_names)
-        b = 0
-        for i, j in self._batches(sizes, self.half, 1 << 30):
+        for b, ((i, j, (flat, host_off, ioff, names, job_sz)), idx) in enumerate(zip(plans, idxs)):
             h = b % 2
             base = h * self.half
-            flat, host_off, ioff, names, job_sz = build_copy_plan(
-                self.layer_names, self.group_idxs, self.layer_bpbs, offsets[i:j],
-                block_ids_list[i:j], layer_name)
             stg = np.cumsum([0] + job_sz[:-1]).astype(np.int64) + base
             if pipe.half_free[h] is not None:
                 pipe.dma.wait_event(pipe.half_free[h])
@@ -257,8 +326,6 @@ class KVIOContext:
             arrived = torch.cuda.Event()
             arrived.record(pipe.dma)
             pipe.kernels.wait_event(arrived)
-            with torch.cuda.stream(pipe.kernels):
-                idx = torch.from_numpy(flat).to(self.device, non_blocking=False)
             if rerotate is None:
                 self.read_copier.scatter_pages(names, stg.tolist(), job_sz, idx, ioff,
                                                pipe.kernels.cuda_stream)
@@ -271,7 +338,6 @@ class KVIOContext:
             ev = torch.cuda.Event()
             ev.record(pipe.kernels)
             pipe.half_free[h] = ev
-            b += 1
         self.done = torch.cuda.Event()
         self.done.record(pipe.kernels)
         return saved

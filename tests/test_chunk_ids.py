@@ -5,6 +5,8 @@ import struct
 
 import pytest
 import xxhash
+from hypothesis import given, settings
+from hypothesis import strategies as st
 
 from daric_amd import chunk_ids as ci
 
@@ -46,5 +48,36 @@ def test_independent_chain_is_position_free():
     ids_b = [cid for cid, (s, e) in b if s >= 5 and e <= 21]
     # group 2 starts a new chain: its pieces get the same ids wherever the group sits
     assert ids_a == ids_b[: len(ids_a)] and len(ids_a) == 4
-    with pytest.raises(AssertionError):
+    with pytest.raises(ValueError):
         ci.independent_chunk_ids([1, 2, 3], [0, 4], 4, "m")
+    with pytest.raises(OverflowError):
+        ci.token_ids_to_bytes([-1])
+
+
+@settings(max_examples=300, deadline=None, derandomize=True)
+@given(groups=st.lists(st.integers(0, 40), min_size=1, max_size=8), m=st.integers(1, 9))
+def test_pieces_tile_the_cached_groups(groups, m):
+    """Pieces are at most m tokens, never cross a group boundary, cover every
+    group but the last completely, and the last group in whole pieces only."""
+    ptr = [0]
+    for n in groups:
+        ptr.append(ptr[-1] + n)
+    bounds, gb = ci.split_chunk_ptr(ptr, m)
+    assert gb == ptr and bounds[0] == 0
+    lens = [b - a for a, b in zip(bounds, bounds[1:])]
+    assert all(1 <= n <= m for n in lens)
+    for a, b in zip(bounds, bounds[1:]):
+        g = max(i for i in range(len(groups)) if ptr[i] <= a)
+        assert b <= ptr[g + 1], "a piece crosses a group boundary"
+    cached = sum(groups[:-1]) + groups[-1] - groups[-1] % m
+    assert bounds[-1] == cached
+    for i, n in enumerate(groups):
+        inside = [x for x in lens_in(bounds, ptr[i], ptr[i + 1])]
+        if i < len(groups) - 1:
+            assert sum(inside) == n and all(x == m for x in inside[:-1])
+        else:
+            assert all(x == m for x in inside)
+
+
+def lens_in(bounds, lo, hi):
+    return [b - a for a, b in zip(bounds, bounds[1:]) if lo <= a and b <= hi]

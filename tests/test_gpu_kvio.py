@@ -3,6 +3,8 @@ restatement of the daric-store GPU I/O (oracle/kvio.py): host record bytes
 and headers bit-exact after store, cache bytes bit-exact after load, the
 fused re-rotating load within the rotation bar; small staging halves force
 multi-batch pipelining and reuse of both halves."""
+import time
+
 import numpy as np
 import pytest
 import torch
@@ -245,3 +247,58 @@ if KV_FUZZ is not None:
         assert got == want == saved
         for n in names:
             assert same_bytes(fresh_dev[n], fresh_cpu[n])
+
+
+def test_concurrent_stores_take_turns_and_close_drains(dev):
+    """Four threads store disjoint records through one context at once: the
+    store lock makes them take turns on the shared staging, so every record
+    matches the oracle's. close() then waits for a running load and its device
+    work; afterwards store and load raise, and a second close() does nothing."""
+    import threading
+    names, cpu, pf, bpb, groups = setup(dev, n_layers=2)
+    rng = np.random.default_rng(3)
+    blocks = metas_blocks(rng, 12, 64, False)
+    dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
+    host_size = 64 << 20
+    host = torch.zeros(host_size, dtype=torch.uint8, pin_memory=True)
+    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * len(names), dev_caches, host,
+                            staging_bytes=512 << 10)
+    offs, end = record_offsets(ctx, blocks)
+    saved = [int(x) for x in rng.integers(0, 1 << 40, len(blocks))]
+    errors = []
+
+    def store(part):
+        try:
+            sel = list(range(part, len(blocks), 4))
+            ctx.store([offs[i] for i in sel], [blocks[i] for i in sel], [saved[i] for i in sel])
+        except Exception as e:  # surfaced below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=store, args=(p,)) for p in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    shm = torch.zeros(host_size, dtype=torch.uint8)
+    okv.OracleKVIO(names, groups, bpb, [pf] * len(names), cpu, shm).store(offs, blocks, saved)
+    assert torch.equal(host, shm)
+    # close while a load is running in another thread
+    fresh = {n: torch.zeros_like(t, device=dev) for n, t in cpu.items()}
+    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * len(names), fresh, host, staging_bytes=512 << 10)
+    got = {}
+    loader = threading.Thread(target=lambda: got.setdefault("saved", ctx2.load(offs, blocks)))
+    loader.start()
+    while not got and ctx2._inflight == 0 and loader.is_alive():
+        time.sleep(0.0005)
+    ctx2.close()
+    loader.join()
+    assert ctx2.closed and got["saved"] == saved
+    loaded = sorted({b for bl in blocks for b in bl[0]})
+    for n in names:
+        assert torch.equal(fresh[n][:, loaded].cpu().view(torch.int16), cpu[n][:, loaded].view(torch.int16))
+    with pytest.raises(RuntimeError, match="closed"):
+        ctx2.load(offs, blocks)
+    with pytest.raises(RuntimeError, match="closed"):
+        ctx2.store(offs, blocks, saved)
+    ctx2.close()

@@ -201,3 +201,25 @@ def test_deviation_fp8_with_scales(dev, layout):
     sel_g = cache_ops.topk_per_chunk(keys_g, chunks, kmax=kmax)
     torch.cuda.synchronize()
     assert np.array_equal(sel_g.cpu().numpy(), sel_o)
+
+
+def test_deviation_allocated_keys_on_a_side_stream(dev):
+    """kv_deviation allocating its own keys while launching on another stream:
+    the zero fill is ordered before the kernel, so the rows outside every
+    chunk read 0 and the chunk rows match the oracle."""
+    layers, pf, bt, chunks, k_new, v_new = setup_case(dev, "nhd", chunk_tokens=(100, 64, 37))
+    cpu = [t for t, _ in layers]
+    gpu = [to_dev(t, dev) for t in cpu]
+    # leave rows 0..9 and the rows after the last chunk outside every chunk
+    T = k_new.shape[1] + 24
+    kn = torch.zeros(k_new.shape[0], T, *k_new.shape[2:], dtype=k_new.dtype)
+    kn[:, 10:10 + k_new.shape[1]] = k_new
+    moved = [(bo, ro + 10, n, k) for (bo, ro, n, k) in chunks]
+    side = torch.cuda.Stream()
+    btd, knd = torch.from_numpy(bt).to(dev), kn.to(dev)
+    torch.cuda.synchronize()
+    keys = cache_ops.kv_deviation(gpu, pf, btd, knd, moved, stream=side.cuda_stream)
+    side.synchronize()
+    want = osel.deviation(cpu, pf, bt, kn, moved)
+    assert np.array_equal(keys.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    assert not keys[:, :10].any() and not keys[:, 10 + k_new.shape[1]:].any()

@@ -72,3 +72,22 @@ def test_record_bytes_and_header():
         for b in range(6):
             same = torch.equal(fresh[n][:, b], layers[n][:, b])
             assert same == (b in (1, 3)) or (b not in (1, 3) and int(fresh[n][:, b].sum()) == 0)
+
+
+def test_split_registration_copies_product_matches_oracle_on_random_regions():
+    rng = np.random.default_rng(8)
+    for _ in range(300):
+        n = int(rng.integers(0, 6))
+        chunk = int(rng.integers(1, 64))
+        stg = rng.integers(0, 500, n).tolist()
+        host = rng.integers(0, 500, n).tolist()
+        size = rng.integers(0, 200, n).tolist()
+        assert kv_io.split_registration_copies(stg, host, size, chunk_bytes=chunk) == \
+            okv.split_registration_copies(stg, host, size, chunk_bytes=chunk)
+    for bad in (([0], [0, 1], [1]), ([-1], [0], [1]), ([0], [0], [-4])):
+        for fn in (kv_io.split_registration_copies, okv.split_registration_copies):
+            try:
+                fn(*bad, chunk_bytes=8)
+            except ValueError:
+                continue
+            raise AssertionError(f"{fn.__module__} accepted {bad}")
