@@ -13,7 +13,10 @@ from ctypes import POINTER, c_char_p, c_double, c_int, c_int32, c_int64, c_uint6
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libdaric_cache_ops.so")
+# DARIC_AMD_LIB selects another build of the same library (the host-sanitized
+# build of `python -m daric_amd.build --sanitize`); unset, the in-tree build.
+LIB_PATH = os.environ.get("DARIC_AMD_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "_lib", "libdaric_cache_ops.so")
 MAX_DIMS = 8
 ABI_VERSION = 4
 ERR_VALUE = 5
