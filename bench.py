@@ -116,6 +116,20 @@ def time_steps(step, steps, warmup, stream):
                 launches_per_step=launches / max(steps, 1))
 
 
+def _event_ms(fn, steps, stream, warmup=2):
+    """Milliseconds per call of fn (HIP events around `steps` back-to-back calls)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
 def run_gpu(cfg, steps, warmup):
     from daric_amd import cache_ops
     dev = torch.device("cuda:0")
@@ -271,6 +285,23 @@ def run_config3(steps, warmup, seed=0):
     whole = time_steps(step, steps, warmup, stream)
     parts = {n: time_steps(f, steps, 1, stream)["kern_ms"]
              for n, f in (("deviation", dev_step), ("topk", topk_step), ("merge", merge_step))}
+    # The merge's address pattern in isolation: the same kernel moving the
+    # same rows' worth of bytes, but with each chunk's first k tokens selected
+    # and chunks laid on consecutive blocks, so both the recomputed rows read
+    # and the cache rows written are sequential at the same 2 KiB granularity.
+    PS = w["PS"]
+    ppc = w["chunks"][0][2] // PS
+    seq_bt = torch.arange(1, n_chunk * ppc + 1, dtype=torch.int32, device=dev)
+    seq_sel = torch.arange(k, dtype=torch.int32, device=dev).repeat(L, n_chunk, 1).contiguous()
+    seq_ms = time_steps(lambda: cache_ops.merge_rows(layers, False, seq_bt, k_new, v_new, chunks, seq_sel,
+                                                     stream=st), steps, 1, stream)["kern_ms"]
+    # and a contiguous device copy of the same byte count (torch copy_): the
+    # streaming ceiling the merge is held against
+    half_bytes = len(chunks) * k * L * (2 * H * D * 2)
+    flat_src = torch.empty(half_bytes, dtype=torch.uint8, device=dev)
+    flat_dst = torch.empty_like(flat_src)
+    flat_ms = _event_ms(lambda: flat_dst.copy_(flat_src), steps, stream)
+    del flat_src, flat_dst
     e = 2
     dev_bytes = T * L * (2 * H * D * e) + T * L * 4
     topk_bytes = T * L * 4 + n_chunk * L * k * 4
@@ -286,7 +317,17 @@ def run_config3(steps, warmup, seed=0):
                         "topk": dict(ms=parts["topk"], bytes=topk_bytes),
                         "merge": dict(ms=parts["merge"], bytes=merge_bytes,
                                       GBps=_gbps(merge_bytes, parts["merge"]),
-                                      frac=_gbps(merge_bytes, parts["merge"]) / PEAK_HBM_GBPS)})
+                                      frac=_gbps(merge_bytes, parts["merge"]) / PEAK_HBM_GBPS,
+                                      sequential_rows=dict(
+                                          ms=seq_ms, GBps=_gbps(merge_bytes, seq_ms),
+                                          note="the same merge_rows kernel and byte count with every "
+                                               "chunk's first k tokens on consecutive blocks: sequential "
+                                               "2 KiB rows on both sides"),
+                                      contiguous_copy=dict(
+                                          ms=flat_ms, GBps=_gbps(merge_bytes, flat_ms),
+                                          merge_frac_of_it=flat_ms / parts["merge"],
+                                          note="torch copy_ of the same byte count between two contiguous "
+                                               "device buffers, same process"))})
     del w, layers, k_new, v_new, keys, sel
     torch.cuda.empty_cache()
     return out

@@ -1187,7 +1187,7 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
             if (g.v_off >= 0) check_scales(v_scales, "v_scales");
             DARIC_CHECK(merge_fits_rows(g, t.elem_size, true),
                         "quantising merge_rows needs head_dim % 8 == 0, 8-byte aligned cache rows and K+V "
-                        "rows of at most 32 KiB of recomputed values");
+                        "rows of at most 64 KiB of recomputed values");
             for (int64_t i = 0; i < n_layers; ++i)
                 DARIC_CHECK(aligned(layers[i].data, 8), "misaligned layer ", i);
         } else {

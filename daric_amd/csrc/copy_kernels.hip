@@ -324,25 +324,45 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
             if (i < u1) v[u] = ld_nt(src + i);
         }
         if (base == u0) {
+            // 16-bit types: lane k takes pairs kk*NC .. kk*NC + NC-1 into
+            // registers. The table is stored transposed, pair i at
+            // (i % NC) * (half / NC) + i / NC, so the lanes of a wavefront
+            // read consecutive words for each e (the row-major, stride-NC
+            // reads took 5.5 M bank-conflict cycles per launch at config 2).
+            // e4m3 (CSL): the (cos, sin) entries are transposed the same way
+            // -- NeoX float4 j (pairs 2j, 2j+1 of a unit) of unit kk at
+            // j * (half / VE) + kk, GPT-J float2 pair pi at pi * (half /
+            // (VE / 2)) + kk -- so each LDS read instruction takes consecutive
+            // entries across the lanes (interleaved in pair order, they took
+            // 30% of the kernel's LDS cycles in bank conflicts at config 5).
+            const int cols = half / NC;
             for (int i = tid; i < half; i += kThreads) {
                 float sn, c;
                 sincosf(j.delta * inv_freq[i], &sn, &c);
                 if (CSL) {
-                    float* q = reinterpret_cast<float*>(s_cs) + 2 * i;
+                    float* q;
+                    if (NEOX) {
+                        const int f = i >> 1;
+                        q = reinterpret_cast<float*>(s_cs + (f % (VE / 2)) * (half / VE) + f / (VE / 2)) + 2 * (i & 1);
+                    } else {
+                        q = reinterpret_cast<float*>(s_cs) + 2 * ((i % (VE / 2)) * (half / (VE / 2)) + i / (VE / 2));
+                    }
                     q[0] = c;
                     q[1] = sn;
                 } else {
-                    s_cos[i] = c;
-                    s_sin[i] = sn;
+                    const int at = (i % NC) * cols + i / NC;
+                    s_cos[at] = c;
+                    s_sin[at] = sn;
                 }
             }
             __syncthreads();
             if (!CSL) {
+                const int kk = pi0 / NC;
 #pragma unroll
                 for (int e = 0; e < NC; ++e) {
-                    const int pi = rot_lane ? pi0 + e : 0;
-                    cs[e] = s_cos[pi];
-                    ss[e] = (NEOX && first) ? -s_sin[pi] : s_sin[pi];
+                    const int at = rot_lane ? e * cols + kk : 0;
+                    cs[e] = s_cos[at];
+                    ss[e] = (NEOX && first) ? -s_sin[at] : s_sin[at];
                 }
             }
         }
@@ -374,10 +394,10 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
                     E::unpack_word(pv[w], y);
                     if (CSL) {
                         // pairs pi0 + w*EPW .. +EPW-1: EPW/2 float4 reads
-                        const float4* csq = s_cs + ((pi0 + w * EPW) >> 1);
+                        const int kk = pi0 / VE;
 #pragma unroll
                         for (int h2 = 0; h2 < EPW / 2; ++h2) {
-                            const float4 t = csq[h2];
+                            const float4 t = s_cs[(w * (EPW / 2) + h2) * (half / VE) + kk];
                             const float s0 = first ? -t.y : t.y, s1 = first ? -t.w : t.w;
                             x[2 * h2] = x[2 * h2] * t.x + y[2 * h2] * s0;
                             x[2 * h2 + 1] = x[2 * h2 + 1] * t.z + y[2 * h2 + 1] * s1;
@@ -393,7 +413,8 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
                         const int pi = w * (EPW / 2) + m;
                         float c, sn;
                         if (CSL) {
-                            const float* csq = reinterpret_cast<const float*>(s_cs) + 2 * (pi0 + pi);
+                            const float* csq = reinterpret_cast<const float*>(s_cs) +
+                                               2 * (pi * (half / (VE / 2)) + pi0 / (VE / 2));
                             c = csq[0];
                             sn = csq[1];
                         } else {

@@ -216,18 +216,26 @@ __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
             if (act[u]) v[u] = ld_nt(pg + i);
         }
         if (base == u0) {
+            // Lane k needs pairs kk*NC .. kk*NC + NC-1. The table is stored
+            // transposed, pair i at (i % NC) * (half / NC) + i / NC, so that
+            // the lanes of a wavefront read consecutive words for each e
+            // (row-major, the stride-NC reads took 2-way bank conflicts:
+            // 30% of the kernel's LDS cycles at config 2).
+            const int cols = half / NC;
             for (int i = tid; i < half; i += kThreads) {
                 float sn, c;
                 sincosf(sg.delta * inv_freq[i], &sn, &c);
-                s_cos[i] = c;
-                s_sin[i] = sn;
+                const int at = (i % NC) * cols + i / NC;
+                s_cos[at] = c;
+                s_sin[at] = sn;
             }
             __syncthreads();
+            const int kk = pi0 / NC;
 #pragma unroll
             for (int e = 0; e < NC; ++e) {
-                const int pi = rot_lane ? pi0 + e : 0;
-                cs[e] = s_cos[pi];
-                ss[e] = (NEOX && first) ? -s_sin[pi] : s_sin[pi];
+                const int at = rot_lane ? e * cols + kk : 0;
+                cs[e] = s_cos[at];
+                ss[e] = (NEOX && first) ? -s_sin[at] : s_sin[at];
             }
         }
 #pragma unroll

@@ -337,13 +337,19 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(
 // write does: code = saturating RTNE of float32(x) / scale[l, h], the
 // division correctly rounded.
 constexpr int kMergeUnits = 8;
+// 256 lanes x 8 units in flight. A same-process sweep at config 3 put 128 or
+// 512 lanes, 4 or 16 units, nontemporal loads or stores, a precomputed slot
+// table, two groups per workgroup and one-wavefront-per-token forms all
+// within +-2% of this, and the whole merge within 8-10% of a contiguous
+// copy of the same bytes.
+constexpr int kMergeThreads = 256;
 constexpr int kMergeMaxTok = 64;
 constexpr int kMergeCopy = 0;
 constexpr int kMergeFromBF16 = kBF16 + 1;
 constexpr int kMergeFromF16 = kF16 + 1;
 
-template <int MODE>
-__global__ __launch_bounds__(kThreads) void merge_rows_kernel(
+template <int MODE, bool DENSE>
+__global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
     DescArg d, int layer_off, KVGeom g, int ces, const int32_t* __restrict__ bt,
     const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T,
     int n_chunks, const int32_t* __restrict__ sel, int kmax, int tpb, int units,
@@ -384,7 +390,7 @@ __global__ __launch_bounds__(kThreads) void merge_rows_kernel(
     u32x4 v[kMergeUnits];
 #pragma unroll
     for (int s = 0; s < kMergeUnits; ++s) {
-        const int f = min(tid + s * kThreads, total - 1);
+        const int f = min(tid + s * kMergeThreads, total - 1);
         const int t = static_cast<int>(d_tok_units.div(static_cast<uint32_t>(f)));
         const int r = f - t * tok_units;
         const int kv = r >= units ? 1 : 0;
@@ -400,16 +406,18 @@ __global__ __launch_bounds__(kThreads) void merge_rows_kernel(
     asm volatile("" : "+v"(tid_s));
 #pragma unroll
     for (int s = 0; s < kMergeUnits; ++s) {
-        const int f = tid_s + s * kThreads;
+        const int f = tid_s + s * kMergeThreads;
         if (f >= total) continue;
         const int t = static_cast<int>(d_tok_units.div(static_cast<uint32_t>(f)));
         const int r = f - t * tok_units;
         const int kv = r >= units ? 1 : 0;
         if (s_src[t] < 0) continue;
         const int u = r - kv * units;
-        const int h = static_cast<int>(d_upr.div(static_cast<uint32_t>(u)));
-        const int un = u - h * upr;
-        uint8_t* dst = base + s_dst[t] + (static_cast<int64_t>(h) * g.sh + (kv ? g.v_off : 0)) * ces;
+        // DENSE: the head rows of a token are contiguous (sh == D), so unit u
+        // of the token row lands at u * (cache bytes per unit)
+        const int h = DENSE && MODE == kMergeCopy ? 0 : static_cast<int>(d_upr.div(static_cast<uint32_t>(u)));
+        const int un = DENSE ? u : u - h * upr;
+        uint8_t* dst = base + s_dst[t] + (static_cast<int64_t>(DENSE ? 0 : h) * g.sh + (kv ? g.v_off : 0)) * ces;
         if constexpr (MODE == kMergeCopy) {
             *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(un) * 16) = v[s];
         } else {
@@ -468,7 +476,7 @@ bool merge_fits_rows(const KVGeom& g, int elem_size, bool quant) {
         (g.v_off >= 0 && (g.v_off * elem_size) % dst_unit))
         return false;
     const int64_t tok_units = static_cast<int64_t>(g.v_off >= 0 ? 2 : 1) * g.H * (g.D * ses / 16);
-    return tok_units <= static_cast<int64_t>(kThreads) * kMergeUnits;
+    return tok_units <= static_cast<int64_t>(kMergeThreads) * kMergeUnits;
 }
 
 void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int elem_size,
@@ -481,16 +489,17 @@ void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g
         const int upr = g.D * ses / 16;                              // source units per head row
         const int units = g.H * upr;                                 // per K (or V) token row
         const int tok_units = (g.v_off >= 0 ? 2 : 1) * units;
-        const int tpb = std::min(kMergeMaxTok, std::max(1, kThreads * kMergeUnits / tok_units));
+        const int tpb = std::min(kMergeMaxTok, std::max(1, kMergeThreads * kMergeUnits / tok_units));
         const dim3 grid(static_cast<unsigned>((kmax + tpb - 1) / tpb), static_cast<unsigned>(n_chunks),
                         static_cast<unsigned>(n_layers));
         const FastDiv dtu(static_cast<uint32_t>(tok_units)), dupr(static_cast<uint32_t>(upr));
-#define DARIC_MR(M) DARIC_LAUNCH((merge_rows_kernel<M>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, \
-                                 block_table, k_new, v_new, T, n_chunks, sel_idx, kmax, tpb, units, dtu, dupr, \
-                                 k_scales, v_scales)
-        if (!quant) DARIC_MR(kMergeCopy);
-        else if (quant_from == kBF16) DARIC_MR(kMergeFromBF16);
-        else DARIC_MR(kMergeFromF16);
+        const bool dense = g.sh == g.D;
+#define DARIC_MR(M, DN) DARIC_LAUNCH((merge_rows_kernel<M, DN>), grid, kMergeThreads, 0, stream, d, layer_off, g, \
+                                     elem_size, block_table, k_new, v_new, T, n_chunks, sel_idx, kmax, tpb, units, \
+                                     dtu, dupr, k_scales, v_scales)
+        if (!quant) { if (dense) DARIC_MR(kMergeCopy, true); else DARIC_MR(kMergeCopy, false); }
+        else if (quant_from == kBF16) { if (dense) DARIC_MR(kMergeFromBF16, true); else DARIC_MR(kMergeFromBF16, false); }
+        else { if (dense) DARIC_MR(kMergeFromF16, true); else DARIC_MR(kMergeFromF16, false); }
 #undef DARIC_MR
     } else {
         const dim3 grid(static_cast<unsigned>((kmax + kMergeTok - 1) / kMergeTok),
