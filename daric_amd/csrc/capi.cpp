@@ -653,6 +653,208 @@ int daric_copier_scatter_tokens(daric_copier* c, const char* const* names, int64
 
 namespace {
 
+// ---- in-place re-rotation planning (shared with daric_rerotate_pages)
+
+// All layers of one call must share shape, strides, dtype and device.
+void check_same_layers(const daric_tensor* layers, int64_t n) {
+    const daric_tensor& a = layers[0];
+    for (int64_t i = 1; i < n; ++i) {
+        const daric_tensor& b = layers[i];
+        bool same = a.ndim == b.ndim && a.dtype == b.dtype && a.elem_size == b.elem_size &&
+                    a.device == b.device;
+        for (int d = 0; same && d < a.ndim; ++d)
+            same = a.sizes[d] == b.sizes[d] && a.strides[d] == b.strides[d];
+        DARIC_CHECK(same, "all layers of one call must share shape, strides, dtype and device; layer ", i,
+                    " differs");
+    }
+}
+
+void check_block_table(const daric_tensor* bt, int device) {
+    check_tensor_struct(bt, "block_table");
+    DARIC_CHECK(bt->device == device, "block_table must be on the layers' device");
+    DARIC_CHECK(bt->ndim == 1 && bt->dtype == DARIC_DTYPE_INT32 && is_contiguous(*bt),
+                "block_table must be a 1-D contiguous int32 tensor");
+}
+
+std::vector<uint8_t*> layer_ptrs(const daric_tensor* layers, int64_t n) {
+    std::vector<uint8_t*> v(n);
+    for (int64_t i = 0; i < n; ++i) v[i] = static_cast<uint8_t*>(layers[i].data);
+    return v;
+}
+
+// A validated in-place rotation: the geometry, kernel path and descriptor
+// bytes (segments, then the layer pointer table) of one call.
+struct InplacePlan {
+    InplaceGeom g{};
+    std::vector<uint8_t> blob;
+    int seg_bytes = 0, n_layers = 0, n_segs = 0, path = kRotElem, kind = 0, device = -1;
+    int64_t tiles = 0;
+    bool neox = false;
+    const int32_t* block_table = nullptr;
+    const float* inv_freq = nullptr;
+};
+
+// Every check of daric_rerotate_pages, and the plan of its launch; no device
+// work. Segments with no tokens or no shift are dropped (n_segs may be 0).
+// min_block: block ids below it are skipped (1 also skips the null block).
+InplacePlan plan_inplace(const daric_tensor* layers, int64_t n_layers, int page_first,
+                     const daric_tensor* block_table, const daric_rope_segment* segments,
+                     int64_t n_segments, const daric_rope* rope, const daric_tensor* k_scales,
+                     int min_block) {
+    InplacePlan plan;
+    DARIC_CHECK(n_layers > 0 && layers != nullptr, "layers must not be empty");
+    DARIC_CHECK(n_segments > 0 && segments != nullptr, "segments must not be null");
+    check_rope(rope);
+    for (int64_t i = 0; i < n_layers; ++i) check_tensor_struct(&layers[i], "kv layer");
+    check_same_layers(layers, n_layers);
+    const daric_tensor& t = layers[0];
+    DARIC_CHECK(t.device >= 0, "KV cache tensor must be on CUDA");
+    const int kind = elem_kind(t);
+    DARIC_CHECK(kind >= 0, "unsupported KV cache dtype for rerotate");
+    const RopeLayout L = rope_layout(t, page_first != 0, rope->rotary_dim);
+    check_block_table(block_table, t.device);
+    const int64_t bt_n = numel(*block_table);
+    if (k_scales != nullptr && k_scales->data != nullptr) {
+        DARIC_CHECK(k_scales->device == t.device && k_scales->dtype == DARIC_DTYPE_FLOAT32 &&
+                    is_contiguous(*k_scales) && numel(*k_scales) == n_layers * L.H,
+                    "k_scales must be a contiguous float32 [n_layers, H] tensor on the layers' device");
+    }
+    const bool neox = rope->is_neox != 0;
+    const int64_t e = t.elem_size;
+    const int64_t VE = kind == kE4M3 ? 16 : 8;
+    const int64_t half = rope->rotary_dim / 2;
+    bool vec = (L.sb * e) % 16 == 0 && (L.ss * e) % 16 == 0 && (L.sh * e) % 16 == 0 &&
+               (neox ? half % VE == 0 : rope->rotary_dim % VE == 0);
+    for (int64_t i = 0; i < n_layers && vec; ++i) vec = aligned(layers[i].data, 16);
+
+    InplaceGeom& g = plan.g;
+    g.min_block = min_block;
+    g.sb = L.sb; g.ss = L.ss; g.sh = L.sh;
+    g.PS = static_cast<int32_t>(L.PS);
+    g.H = static_cast<int32_t>(L.H);
+    g.R = rope->rotary_dim;
+    g.num_blocks = static_cast<int32_t>(L.num_blocks);
+    g.n_rot = static_cast<int32_t>(vec ? (neox ? half / VE : rope->rotary_dim / VE) : half);
+    const int64_t per_tok = L.H * g.n_rot;
+    // about 1024 items (vector path) or 2048 pairs (element path) per tile
+    const int64_t tile_items = vec ? 1024 : 2048;
+    g.tile_tokens = static_cast<int32_t>(std::max<int64_t>(1, tile_items / std::max<int64_t>(per_tok, 1)));
+    // Page tiles (rerotate_lane_kernel) when a page's K rows are dense
+    // rows of a power-of-two number (<= 64) of 16-byte units.
+    int path = vec ? kRotVec : kRotElem;
+    if (vec) {
+        const int64_t W = L.row_width;
+        const int64_t upr = W * e / 16;
+        int64_t tok_div = 0;
+        if (L.H == 1 && L.ss == W) tok_div = 1;
+        else if (L.H > 1 && L.ss == L.H * W && L.sh == W) tok_div = L.H;     // [PS, H, W] rows
+        else if (L.H > 1 && L.sh == L.PS * W && L.ss == W) tok_div = 1;      // [H, PS, W] rows
+        if (tok_div > 0 && (W * e) % 16 == 0 && upr > 0 && upr <= 64 && (upr & (upr - 1)) == 0 &&
+            L.PS * L.H * upr <= kIntMax) {
+            path = kRotLane;
+            g.upr = static_cast<int32_t>(upr);
+            g.tok_div = static_cast<int32_t>(tok_div);
+            // page tiles in parts of at least 16 KiB (whole rows each): two
+            // halves of a 32 KiB bf16 K page measured ~1% faster at config 2
+            const int64_t units = L.PS * L.H * upr;
+            int lp = 0;
+            while ((units >> (lp + 1)) * 16 >= 16384 && units % (2ll << lp) == 0 &&
+                   (units >> (lp + 1)) % upr == 0)
+                ++lp;
+            g.log2_parts = lp;
+        }
+    }
+
+    std::vector<RopeSeg> segs;
+    int64_t tiles = 0;
+    for (int64_t i = 0; i < n_segments; ++i) {
+        const daric_rope_segment& s = segments[i];
+        DARIC_CHECK(s.n_tokens >= 0 && s.tok_start >= 0 && s.bt_offset >= 0,
+                    "negative segment field at segment ", i);
+        DARIC_CHECK(s.delta > -(1ll << 24) && s.delta < (1ll << 24), "delta out of range at segment ", i);
+        if (s.n_tokens == 0 || s.delta == 0) continue;
+        DARIC_CHECK(s.tok_start + s.n_tokens <= kIntMax, "segment too long at segment ", i);
+        const int64_t last_block = (s.tok_start + s.n_tokens - 1) / L.PS;
+        DARIC_CHECK(s.bt_offset + last_block < bt_n, "segment ", i,
+                    " reads past the end of block_table");
+        RopeSeg rs{};
+        rs.bt_offset = s.bt_offset;
+        rs.tok_start = static_cast<int32_t>(s.tok_start);
+        rs.n_tokens = static_cast<int32_t>(s.n_tokens);
+        rs.delta = static_cast<float>(s.delta);
+        rs.tile_begin = static_cast<int32_t>(tiles);
+        if (path == kRotLane)
+            tiles += (last_block - s.tok_start / L.PS + 1) << g.log2_parts;   // the pages the segment touches
+        else
+            tiles += (s.n_tokens + g.tile_tokens - 1) / g.tile_tokens;
+        segs.push_back(rs);
+    }
+    DARIC_CHECK(tiles <= kMaxTiles, "too many tokens in one rerotate call");
+    if (segs.empty()) return plan;
+    const size_t seg_bytes = segs.size() * sizeof(RopeSeg);
+    plan.blob.resize(seg_bytes + n_layers * sizeof(uint8_t*));
+    std::memcpy(plan.blob.data(), segs.data(), seg_bytes);
+    const auto ptrs = layer_ptrs(layers, n_layers);
+    std::memcpy(plan.blob.data() + seg_bytes, ptrs.data(), n_layers * sizeof(uint8_t*));
+    plan.seg_bytes = static_cast<int>(seg_bytes);
+    plan.n_layers = static_cast<int>(n_layers);
+    plan.n_segs = static_cast<int>(segs.size());
+    plan.path = path;
+    plan.kind = kind;
+    plan.device = t.device;
+    plan.tiles = tiles;
+    plan.neox = neox;
+    plan.block_table = static_cast<const int32_t*>(block_table->data);
+    plan.inv_freq = rope->inv_freq;
+    return plan;
+}
+
+void launch_inplace(const InplacePlan& p, hipStream_t st) {
+    DescHandOver ho(p.device, p.blob.data(), p.blob.size(), st);
+    launch_rerotate_inplace(ho.arg(), p.seg_bytes, p.n_layers, p.g, p.n_segs, static_cast<int>(p.tiles),
+                            p.block_table, p.inv_freq, p.kind, p.neox, p.path, st);
+}
+
+
+// scatter_pages_rerotate for layouts the fused kernel does not take: the
+// jobs are scattered by the copy kernel, then each layer's moved tokens are
+// rotated in place (one in-place call per layer, over the job's page ids).
+// Pages with id 0 are skipped by both, as the fused kernel skips them. Every
+// rotation is planned, and so validated, before the scatter is enqueued.
+void scatter_then_rotate(const ResolvedJobs& r, const daric_tensor* indices, const int64_t* indices_offsets,
+                         const int64_t* deltas, const int64_t* num_tokens, const daric_rope* rope,
+                         uint64_t stream) {
+    std::vector<daric_copier::Layer*> order;
+    std::unordered_map<daric_copier::Layer*, std::vector<daric_rope_segment>> segs;
+    for (size_t i = 0; i < r.jobs.size(); ++i) {
+        daric_copier::Layer* L = r.layers[i];
+        const int64_t page_tokens = static_cast<int64_t>(r.jobs[i].n_sel) * L->lay.PS;
+        const int64_t n = std::min(num_tokens[i], page_tokens);
+        if (deltas[i] == 0 || n <= 0) continue;
+        auto it = segs.find(L);
+        if (it == segs.end()) {
+            order.push_back(L);
+            it = segs.emplace(L, std::vector<daric_rope_segment>{}).first;
+        }
+        it->second.push_back(daric_rope_segment{indices_offsets[i], 0, n, deltas[i]});
+    }
+    std::vector<InplacePlan> plans;
+    for (daric_copier::Layer* L : order) {
+        const auto& sv = segs[L];
+        InplacePlan p = plan_inplace(&L->t, 1, L->page_first ? 1 : 0, indices, sv.data(),
+                                     static_cast<int64_t>(sv.size()), rope, nullptr, 1);
+        if (p.n_segs > 0) plans.push_back(std::move(p));
+    }
+    DeviceGuard guard(r.device);
+    const hipStream_t st = as_stream(stream);
+    {
+        DescHandOver ho(r.device, r.jobs.data(), r.jobs.size() * sizeof(CopyJob), st);
+        launch_copy_pages(ho.arg(), static_cast<int>(r.jobs.size()), static_cast<int>(r.max_tiles), r.max_span,
+                          r.vw, false, st);
+    }
+    for (const InplacePlan& p : plans) launch_inplace(p, st);
+}
+
 // scatter_pages_rerotate and its allocation-free variant: the same checks
 // and kernels; they differ only in how the job descriptors reach the kernels
 // when they do not fit in the kernel arguments (the ring, or the static
@@ -670,7 +872,10 @@ int scatter_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs, 
         if (r.jobs.empty() || r.max_elements == 0) return;
         check_rope(rope);
         DARIC_CHECK(deltas != nullptr && num_tokens != nullptr, "deltas and num_tokens must not be null");
-        DARIC_CHECK(r.vw == 16, "fused scatter+rerotate needs 16-byte aligned pages, strides and offsets");
+        // The fused kernel needs 16-byte aligned pages and dense K head rows
+        // whose rotated halves are 16-byte multiples; otherwise the call
+        // scatters with the copy kernel and then rotates in place.
+        bool fused = r.vw == 16;
         // Group jobs by row geometry and element type; one launch per group
         // (normally one: every layer of a model shares its geometry).
         struct Group {
@@ -707,8 +912,7 @@ int scatter_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs, 
             DARIC_CHECK(L->k_scale == nullptr || L->k_scale_numel >= L->lay.H,
                         "k_scale of job ", i, " has ", L->k_scale_numel, " entries, the layer has ",
                         L->lay.H, " heads");
-            DARIC_CHECK(L->geom_ok, "fused scatter+rerotate does not support the layout of job ", i, " (",
-                        L->geom_msg, "); use scatter_pages followed by rerotate_pages");
+            fused = fused && L->geom_ok;
             CopyJob& j = r.jobs[i];
             j.delta = static_cast<float>(deltas[i]);
             j.n_tokens = static_cast<int32_t>(std::min<int64_t>(num_tokens[i], kIntMax));
@@ -722,6 +926,12 @@ int scatter_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs, 
             }
             grp->jobs.push_back(j);
             grp->max_tiles = std::max<int64_t>(grp->max_tiles, int64_t(j.prefix) * j.n_sel);
+        }
+        if (!fused) {
+            DARIC_CHECK(!noalloc, "scatter_pages_rerotate_noalloc needs a layout the fused kernel takes "
+                                  "(16-byte aligned pages, dense K head rows, 16-byte rotated halves)");
+            scatter_then_rotate(r, indices, indices_offsets, deltas, num_tokens, rope, stream);
+            return;
         }
         // Allocation-free variant: job sets that do not travel inline are
         // staged in the static scratch array, one region per launch group.
@@ -853,37 +1063,6 @@ int daric_batched_memcpy_h2d(const daric_tensor* shm, const daric_tensor* stagin
 }  // extern "C"
 
 // ====================================================== in-place re-rotation
-namespace {
-
-// All layers of one call must share shape, strides, dtype and device.
-void check_same_layers(const daric_tensor* layers, int64_t n) {
-    const daric_tensor& a = layers[0];
-    for (int64_t i = 1; i < n; ++i) {
-        const daric_tensor& b = layers[i];
-        bool same = a.ndim == b.ndim && a.dtype == b.dtype && a.elem_size == b.elem_size &&
-                    a.device == b.device;
-        for (int d = 0; same && d < a.ndim; ++d)
-            same = a.sizes[d] == b.sizes[d] && a.strides[d] == b.strides[d];
-        DARIC_CHECK(same, "all layers of one call must share shape, strides, dtype and device; layer ", i,
-                    " differs");
-    }
-}
-
-void check_block_table(const daric_tensor* bt, int device) {
-    check_tensor_struct(bt, "block_table");
-    DARIC_CHECK(bt->device == device, "block_table must be on the layers' device");
-    DARIC_CHECK(bt->ndim == 1 && bt->dtype == DARIC_DTYPE_INT32 && is_contiguous(*bt),
-                "block_table must be a 1-D contiguous int32 tensor");
-}
-
-std::vector<uint8_t*> layer_ptrs(const daric_tensor* layers, int64_t n) {
-    std::vector<uint8_t*> v(n);
-    for (int64_t i = 0; i < n; ++i) v[i] = static_cast<uint8_t*>(layers[i].data);
-    return v;
-}
-
-}  // namespace
-
 extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers, int page_first,
                                     const daric_tensor* block_table,
                                     const daric_rope_segment* segments, int64_t n_segments,
@@ -891,107 +1070,11 @@ extern "C" int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers
                                     uint64_t stream) {
     return guarded([&] {
         if (n_layers == 0 || n_segments == 0) return;
-        DARIC_CHECK(n_layers > 0 && layers != nullptr, "layers must not be empty");
-        DARIC_CHECK(n_segments > 0 && segments != nullptr, "segments must not be null");
-        check_rope(rope);
-        for (int64_t i = 0; i < n_layers; ++i) check_tensor_struct(&layers[i], "kv layer");
-        check_same_layers(layers, n_layers);
-        const daric_tensor& t = layers[0];
-        DARIC_CHECK(t.device >= 0, "KV cache tensor must be on CUDA");
-        const int kind = elem_kind(t);
-        DARIC_CHECK(kind >= 0, "unsupported KV cache dtype for rerotate");
-        const RopeLayout L = rope_layout(t, page_first != 0, rope->rotary_dim);
-        check_block_table(block_table, t.device);
-        const int64_t bt_n = numel(*block_table);
-        if (k_scales != nullptr && k_scales->data != nullptr) {
-            DARIC_CHECK(k_scales->device == t.device && k_scales->dtype == DARIC_DTYPE_FLOAT32 &&
-                        is_contiguous(*k_scales) && numel(*k_scales) == n_layers * L.H,
-                        "k_scales must be a contiguous float32 [n_layers, H] tensor on the layers' device");
-        }
-        const bool neox = rope->is_neox != 0;
-        const int64_t e = t.elem_size;
-        const int64_t VE = kind == kE4M3 ? 16 : 8;
-        const int64_t half = rope->rotary_dim / 2;
-        bool vec = (L.sb * e) % 16 == 0 && (L.ss * e) % 16 == 0 && (L.sh * e) % 16 == 0 &&
-                   (neox ? half % VE == 0 : rope->rotary_dim % VE == 0);
-        for (int64_t i = 0; i < n_layers && vec; ++i) vec = aligned(layers[i].data, 16);
-
-        InplaceGeom g{};
-        g.sb = L.sb; g.ss = L.ss; g.sh = L.sh;
-        g.PS = static_cast<int32_t>(L.PS);
-        g.H = static_cast<int32_t>(L.H);
-        g.R = rope->rotary_dim;
-        g.num_blocks = static_cast<int32_t>(L.num_blocks);
-        g.n_rot = static_cast<int32_t>(vec ? (neox ? half / VE : rope->rotary_dim / VE) : half);
-        const int64_t per_tok = L.H * g.n_rot;
-        // about 1024 items (vector path) or 2048 pairs (element path) per tile
-        const int64_t tile_items = vec ? 1024 : 2048;
-        g.tile_tokens = static_cast<int32_t>(std::max<int64_t>(1, tile_items / std::max<int64_t>(per_tok, 1)));
-        // Page tiles (rerotate_lane_kernel) when a page's K rows are dense
-        // rows of a power-of-two number (<= 64) of 16-byte units.
-        int path = vec ? kRotVec : kRotElem;
-        if (vec) {
-            const int64_t W = L.row_width;
-            const int64_t upr = W * e / 16;
-            int64_t tok_div = 0;
-            if (L.H == 1 && L.ss == W) tok_div = 1;
-            else if (L.H > 1 && L.ss == L.H * W && L.sh == W) tok_div = L.H;     // [PS, H, W] rows
-            else if (L.H > 1 && L.sh == L.PS * W && L.ss == W) tok_div = 1;      // [H, PS, W] rows
-            if (tok_div > 0 && (W * e) % 16 == 0 && upr > 0 && upr <= 64 && (upr & (upr - 1)) == 0 &&
-                L.PS * L.H * upr <= kIntMax) {
-                path = kRotLane;
-                g.upr = static_cast<int32_t>(upr);
-                g.tok_div = static_cast<int32_t>(tok_div);
-                // page tiles in parts of at least 16 KiB (whole rows each): two
-                // halves of a 32 KiB bf16 K page measured ~1% faster at config 2
-                const int64_t units = L.PS * L.H * upr;
-                int lp = 0;
-                while ((units >> (lp + 1)) * 16 >= 16384 && units % (2ll << lp) == 0 &&
-                       (units >> (lp + 1)) % upr == 0)
-                    ++lp;
-                g.log2_parts = lp;
-            }
-        }
-
-        std::vector<RopeSeg> segs;
-        int64_t tiles = 0;
-        for (int64_t i = 0; i < n_segments; ++i) {
-            const daric_rope_segment& s = segments[i];
-            DARIC_CHECK(s.n_tokens >= 0 && s.tok_start >= 0 && s.bt_offset >= 0,
-                        "negative segment field at segment ", i);
-            DARIC_CHECK(s.delta > -(1ll << 24) && s.delta < (1ll << 24), "delta out of range at segment ", i);
-            if (s.n_tokens == 0 || s.delta == 0) continue;
-            DARIC_CHECK(s.tok_start + s.n_tokens <= kIntMax, "segment too long at segment ", i);
-            const int64_t last_block = (s.tok_start + s.n_tokens - 1) / L.PS;
-            DARIC_CHECK(s.bt_offset + last_block < bt_n, "segment ", i,
-                        " reads past the end of block_table");
-            RopeSeg rs{};
-            rs.bt_offset = s.bt_offset;
-            rs.tok_start = static_cast<int32_t>(s.tok_start);
-            rs.n_tokens = static_cast<int32_t>(s.n_tokens);
-            rs.delta = static_cast<float>(s.delta);
-            rs.tile_begin = static_cast<int32_t>(tiles);
-            if (path == kRotLane)
-                tiles += (last_block - s.tok_start / L.PS + 1) << g.log2_parts;   // the pages the segment touches
-            else
-                tiles += (s.n_tokens + g.tile_tokens - 1) / g.tile_tokens;
-            segs.push_back(rs);
-        }
-        if (segs.empty()) return;
-        DARIC_CHECK(tiles <= kMaxTiles, "too many tokens in one rerotate call");
-        DeviceGuard guard(t.device);
-        const hipStream_t st = as_stream(stream);
-        // One upload: segments followed by the layer pointer table.
-        const size_t seg_bytes = segs.size() * sizeof(RopeSeg);
-        std::vector<uint8_t> blob(seg_bytes + n_layers * sizeof(uint8_t*));
-        std::memcpy(blob.data(), segs.data(), seg_bytes);
-        const auto ptrs = layer_ptrs(layers, n_layers);
-        std::memcpy(blob.data() + seg_bytes, ptrs.data(), n_layers * sizeof(uint8_t*));
-        DescHandOver ho(t.device, blob.data(), blob.size(), st);
-        launch_rerotate_inplace(ho.arg(), static_cast<int>(seg_bytes), static_cast<int>(n_layers), g,
-                                static_cast<int>(segs.size()), static_cast<int>(tiles),
-                                static_cast<const int32_t*>(block_table->data), rope->inv_freq,
-                                kind, neox, path, st);
+        const InplacePlan p = plan_inplace(layers, n_layers, page_first, block_table, segments, n_segments, rope,
+                                           k_scales, 0);
+        if (p.n_segs == 0) return;
+        DeviceGuard guard(p.device);
+        launch_inplace(p, as_stream(stream));
     });
 }
 
@@ -1130,8 +1213,7 @@ int daric_topk_per_chunk(const daric_tensor* keys, const daric_chunk* chunks, in
         const int64_t kmax = out_idx->sizes[2];
         Chunks c = build_chunks(chunks, n_chunks, 1, kInt64Max, T, 1);
         DARIC_CHECK(c.max_k <= kmax, "out_idx kmax (", kmax, ") is smaller than a chunk's k (", c.max_k, ")");
-        DARIC_CHECK(c.max_tokens <= 8192, "topk_per_chunk supports chunks of at most 8192 tokens");
-        DARIC_CHECK(n_chunks <= kMaxTiles && L <= 65535, "too many chunks or layers");
+        DARIC_CHECK(n_chunks <= kMaxTiles, "too many chunks in one topk_per_chunk call: ", n_chunks);
         if (L == 0 || kmax == 0) return;
         DeviceGuard guard(keys->device);
         const hipStream_t st = as_stream(stream);
@@ -1203,7 +1285,6 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
         const int64_t kmax = sel_idx->sizes[2];
         Chunks c = build_chunks(chunks, n_chunks, g.PS, numel(*block_table), T, 1);
         if (kmax == 0) return;
-        DARIC_CHECK(n_chunks <= 65535 && n_layers <= 65535, "too many chunks or layers for merge_rows");
         DeviceGuard guard(t.device);
         const hipStream_t st = as_stream(stream);
         const size_t cb = c.v.size() * sizeof(SelChunk);

@@ -102,7 +102,7 @@ struct InplaceGeom {
     int32_t upr;       // lane path: 16-byte units per K row (a power of two dividing 64)
     int32_t tok_div;   // lane path: rows per token step (H: token-major rows, 1: head-major)
     int32_t log2_parts;  // lane path: parts per page tile
-    int32_t pad0;
+    int32_t min_block;   // block ids below it are skipped: 0, or 1 to skip the null block too
 };
 
 struct RopeSeg {

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kThreads) void rerotate_vec_kernel(
             const uint32_t pos = pos0 + t;
             const uint32_t q = d_ps.div(pos);
             const int blk = bt[sg.bt_offset + q];
-            if (blk < 0 || blk >= g.num_blocks) continue;
+            if (blk < g.min_block || blk >= g.num_blocks) continue;
             kk[u] = static_cast<int>(rem - h * static_cast<uint32_t>(g.n_rot));
             p[u] = reinterpret_cast<u32x4*>(
                        base + (static_cast<int64_t>(blk) * g.sb +
@@ -184,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
     const int hi = min(sg.tok_start + sg.n_tokens - page_tok0, g.PS);
     if (hi <= lo) return;
     const int blk = bt[sg.bt_offset + page];
-    if (blk < 0 || blk >= g.num_blocks) return;
+    if (blk < g.min_block || blk >= g.num_blocks) return;
     u32x4* __restrict__ pg = reinterpret_cast<u32x4*>(layers[blockIdx.y] + static_cast<int64_t>(blk) * g.sb * ES);
 
     const int tid = static_cast<int>(threadIdx.x);
@@ -316,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void rerotate_elem_kernel(
         const int i = rem - h * half;
         const int pos = sg.tok_start + tok0 + t;
         const int blk = bt[sg.bt_offset + pos / g.PS];
-        if (blk < 0 || blk >= g.num_blocks) continue;
+        if (blk < g.min_block || blk >= g.num_blocks) continue;
         const int64_t row = static_cast<int64_t>(blk) * g.sb +
                             static_cast<int64_t>(pos % g.PS) * g.ss + static_cast<int64_t>(h) * g.sh;
         const int64_t e1 = NEOX ? row + i : row + 2 * i;

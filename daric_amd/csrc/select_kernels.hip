@@ -30,6 +30,8 @@ constexpr int kWaves = kThreads / 64;
 // caches, where the 8-token form measured slower (config 5).
 template <int CK> constexpr int dev_tok_per_wave() { return CK == kE4M3 ? 4 : 8; }
 constexpr int kMergeTok = 8;                       // selected tokens per merge workgroup
+constexpr int kMaxGridYZ = 65535;                  // grid.y / grid.z limit; larger counts are sliced
+constexpr int kTopkLdsTokens = 8192;               // top-k keys staged in LDS up to this chunk length
 
 __device__ __forceinline__ int find_chunk(DescPtr<SelChunk> ch, int n, int tile) {
     int lo = 0, hi = n - 1;
@@ -86,12 +88,12 @@ template <int CK, int NK>
 __global__ __launch_bounds__(kThreads) void deviation_kernel(
     DescArg d, int layer_off, KVGeom g, const int32_t* __restrict__ bt,
     const uint8_t* __restrict__ k_new, int64_t T, int n_chunks,
-    const float* __restrict__ k_scales, float* __restrict__ keys) {
+    const float* __restrict__ k_scales, float* __restrict__ keys, int l0) {
 #pragma clang fp contract(off)
     const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
     constexpr int CES = CK == kE4M3 ? 1 : 2;
-    const int l = static_cast<int>(blockIdx.y);
+    const int l = static_cast<int>(blockIdx.y) + l0;
     const int tile = static_cast<int>(blockIdx.x);
     const SelChunk c = desc_load(chunks + find_chunk(chunks, n_chunks, tile));
     const int lane = static_cast<int>(threadIdx.x) & 63;
@@ -191,16 +193,20 @@ __device__ __forceinline__ int block_excl_count(bool flag, int* s_wave, int* tot
     return before + below;
 }
 
+// LDS_KEYS: the chunk's order keys are staged in LDS (chunks of at most
+// kTopkLdsTokens tokens); otherwise every pass reads them from global memory,
+// where a chunk's keys (4 bytes per token) stay in L2 across the five passes.
+template <bool LDS_KEYS>
 __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ keys, int64_t T,
                                                         DescArg d, int n_chunks,
-                                                        int32_t* __restrict__ out, int kmax) {
+                                                        int32_t* __restrict__ out, int kmax, int l0) {
     const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     extern __shared__ uint32_t s_keys[];
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_digit, s_above;
     __shared__ int s_wave[kWaves];
 
-    const int l = static_cast<int>(blockIdx.y);
+    const int l = static_cast<int>(blockIdx.y) + l0;
     const int ci = static_cast<int>(blockIdx.x);
     const SelChunk c = desc_load(chunks + ci);
     const int n = c.n_tokens;
@@ -211,7 +217,9 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
     for (int i = k + tid; i < kmax; i += kThreads) orow[i] = -1;
     if (k == 0) return;
     const float* krow = keys + static_cast<int64_t>(l) * T + c.row_offset;
-    for (int i = tid; i < n; i += kThreads) s_keys[i] = order_key(krow[i]);
+    if (LDS_KEYS)
+        for (int i = tid; i < n; i += kThreads) s_keys[i] = order_key(krow[i]);
+    const auto key_at = [&](int i) -> uint32_t { return LDS_KEYS ? s_keys[i] : order_key(krow[i]); };
 
     uint32_t prefix = 0, mask = 0, krem = static_cast<uint32_t>(k);
     for (int pass = 0; pass < 4; ++pass) {
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
         // digits of one chunk's keys are nearly all equal).
         for (int b = 0; b < n; b += kThreads) {
             const int i = b + tid;
-            const uint32_t key = i < n ? s_keys[i] : 0u;
+            const uint32_t key = i < n ? key_at(i) : 0u;
             const bool act = i < n && (key & mask) == prefix;
             const uint32_t dig = (key >> shift) & 255u;
             unsigned long long same = __ballot(act);
@@ -269,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
     int running = 0, eq_seen = 0;
     for (int b = 0; b < n; b += kThreads) {
         const int i = b + tid;
-        const uint32_t key = i < n ? s_keys[i] : 0u;
+        const uint32_t key = i < n ? key_at(i) : 0u;
         const bool gt = i < n && key > prefix;
         const bool eq = i < n && key == prefix;
         int eq_total, sel_total;
@@ -286,12 +294,12 @@ template <int VW>
 __global__ __launch_bounds__(kThreads) void merge_kernel(
     DescArg d, int layer_off, KVGeom g, int es, const int32_t* __restrict__ bt,
     const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T,
-    int n_chunks, const int32_t* __restrict__ sel, int kmax) {
+    int n_chunks, const int32_t* __restrict__ sel, int kmax, int c0, int l0) {
     const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
     using V = typename std::conditional<VW == 16, u32x4, uint8_t>::type;
-    const int l = static_cast<int>(blockIdx.z);
-    const int ci = static_cast<int>(blockIdx.y);
+    const int l = static_cast<int>(blockIdx.z) + l0;
+    const int ci = static_cast<int>(blockIdx.y) + c0;
     const SelChunk c = desc_load(chunks + ci);
     const int q0 = static_cast<int>(blockIdx.x) * kMergeTok;
     const int32_t* srow = sel + (static_cast<int64_t>(l) * n_chunks + ci) * kmax;
@@ -354,13 +362,13 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
     const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T,
     int n_chunks, const int32_t* __restrict__ sel, int kmax, int tpb, int units,
     FastDiv d_tok_units, FastDiv d_upr, const float* __restrict__ k_scales,
-    const float* __restrict__ v_scales) {
+    const float* __restrict__ v_scales, int c0, int l0) {
     __shared__ int64_t s_src[kMergeMaxTok];   // byte offset of the token's recomputed rows (-1: skip)
     __shared__ int64_t s_dst[kMergeMaxTok];   // byte offset of the token's K row in the layer
     const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
-    const int l = static_cast<int>(blockIdx.z);
-    const int ci = static_cast<int>(blockIdx.y);
+    const int l = static_cast<int>(blockIdx.z) + l0;
+    const int ci = static_cast<int>(blockIdx.y) + c0;
     const SelChunk c = desc_load(chunks + ci);
     const int tid = static_cast<int>(threadIdx.x);
     const int ses = MODE == kMergeCopy ? ces : 2;                    // source element size
@@ -445,27 +453,35 @@ void launch_deviation(const DescArg& d, int layer_off, int n_layers, const KVGeo
                       const int32_t* block_table, const uint8_t* k_new, int new_kind,
                       int64_t T, int n_chunks, int n_tiles,
                       const float* k_scales, float* keys, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(n_layers));
-#define DARIC_DV(C, N) DARIC_LAUNCH((deviation_kernel<C, N>), grid, kThreads, 0, stream, d, layer_off, g, block_table, k_new, T, n_chunks, k_scales, keys)
-    if (new_kind == kBF16) {
-        if (cache_kind == kBF16) DARIC_DV(kBF16, kBF16);
-        else if (cache_kind == kF16) DARIC_DV(kF16, kBF16);
-        else DARIC_DV(kE4M3, kBF16);
-    } else {
-        if (cache_kind == kBF16) DARIC_DV(kBF16, kF16);
-        else if (cache_kind == kF16) DARIC_DV(kF16, kF16);
-        else DARIC_DV(kE4M3, kF16);
-    }
+    for (int l0 = 0; l0 < n_layers; l0 += kMaxGridYZ) {
+        const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(std::min(kMaxGridYZ, n_layers - l0)));
+#define DARIC_DV(C, N) DARIC_LAUNCH((deviation_kernel<C, N>), grid, kThreads, 0, stream, d, layer_off, g, block_table, k_new, T, n_chunks, k_scales, keys, l0)
+        if (new_kind == kBF16) {
+            if (cache_kind == kBF16) DARIC_DV(kBF16, kBF16);
+            else if (cache_kind == kF16) DARIC_DV(kF16, kBF16);
+            else DARIC_DV(kE4M3, kBF16);
+        } else {
+            if (cache_kind == kBF16) DARIC_DV(kBF16, kF16);
+            else if (cache_kind == kF16) DARIC_DV(kF16, kF16);
+            else DARIC_DV(kE4M3, kF16);
+        }
 #undef DARIC_DV
-    check_launch("kv_deviation");
+        check_launch("kv_deviation");
+    }
 }
 
 void launch_topk(const float* keys, int n_layers, int64_t T, const DescArg& d,
                  int n_chunks, int max_tokens, int32_t* out_idx, int kmax, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
-    const size_t lds = static_cast<size_t>(max_tokens) * sizeof(uint32_t);
-    DARIC_LAUNCH((topk_kernel), grid, kThreads, lds, stream, keys, T, d, n_chunks, out_idx, kmax);
-    check_launch("topk_per_chunk");
+    const bool lds = max_tokens <= kTopkLdsTokens;
+    const size_t lds_bytes = lds ? static_cast<size_t>(max_tokens) * sizeof(uint32_t) : 0;
+    for (int l0 = 0; l0 < n_layers; l0 += kMaxGridYZ) {
+        const dim3 grid(static_cast<unsigned>(n_chunks), static_cast<unsigned>(std::min(kMaxGridYZ, n_layers - l0)));
+        if (lds)
+            DARIC_LAUNCH((topk_kernel<true>), grid, kThreads, lds_bytes, stream, keys, T, d, n_chunks, out_idx, kmax, l0);
+        else
+            DARIC_LAUNCH((topk_kernel<false>), grid, kThreads, 0, stream, keys, T, d, n_chunks, out_idx, kmax, l0);
+        check_launch("topk_per_chunk");
+    }
 }
 
 bool merge_fits_rows(const KVGeom& g, int elem_size, bool quant) {
@@ -484,37 +500,44 @@ void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g
                   int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, int quant_from,
                   const float* k_scales, const float* v_scales, hipStream_t stream) {
     const bool quant = quant_from >= 0;
-    if (merge_fits_rows(g, elem_size, quant)) {
-        const int ses = quant ? 2 : elem_size;
-        const int upr = g.D * ses / 16;                              // source units per head row
-        const int units = g.H * upr;                                 // per K (or V) token row
-        const int tok_units = (g.v_off >= 0 ? 2 : 1) * units;
-        const int tpb = std::min(kMergeMaxTok, std::max(1, kMergeThreads * kMergeUnits / tok_units));
-        const dim3 grid(static_cast<unsigned>((kmax + tpb - 1) / tpb), static_cast<unsigned>(n_chunks),
-                        static_cast<unsigned>(n_layers));
-        const FastDiv dtu(static_cast<uint32_t>(tok_units)), dupr(static_cast<uint32_t>(upr));
-        const bool dense = g.sh == g.D;
+    // grid.y (chunks) and grid.z (layers) are cut into slices of at most 65535
+    for (int l0 = 0; l0 < n_layers; l0 += kMaxGridYZ) {
+        const int nl = std::min(kMaxGridYZ, n_layers - l0);
+        for (int c0 = 0; c0 < n_chunks; c0 += kMaxGridYZ) {
+            const int nc = std::min(kMaxGridYZ, n_chunks - c0);
+            if (merge_fits_rows(g, elem_size, quant)) {
+                const int ses = quant ? 2 : elem_size;
+                const int upr = g.D * ses / 16;                              // source units per head row
+                const int units = g.H * upr;                                 // per K (or V) token row
+                const int tok_units = (g.v_off >= 0 ? 2 : 1) * units;
+                const int tpb = std::min(kMergeMaxTok, std::max(1, kMergeThreads * kMergeUnits / tok_units));
+                const dim3 grid(static_cast<unsigned>((kmax + tpb - 1) / tpb), static_cast<unsigned>(nc),
+                                static_cast<unsigned>(nl));
+                const FastDiv dtu(static_cast<uint32_t>(tok_units)), dupr(static_cast<uint32_t>(upr));
+                const bool dense = g.sh == g.D;
 #define DARIC_MR(M, DN) DARIC_LAUNCH((merge_rows_kernel<M, DN>), grid, kMergeThreads, 0, stream, d, layer_off, g, \
                                      elem_size, block_table, k_new, v_new, T, n_chunks, sel_idx, kmax, tpb, units, \
-                                     dtu, dupr, k_scales, v_scales)
-        if (!quant) { if (dense) DARIC_MR(kMergeCopy, true); else DARIC_MR(kMergeCopy, false); }
-        else if (quant_from == kBF16) { if (dense) DARIC_MR(kMergeFromBF16, true); else DARIC_MR(kMergeFromBF16, false); }
-        else { if (dense) DARIC_MR(kMergeFromF16, true); else DARIC_MR(kMergeFromF16, false); }
+                                     dtu, dupr, k_scales, v_scales, c0, l0)
+                if (!quant) { if (dense) DARIC_MR(kMergeCopy, true); else DARIC_MR(kMergeCopy, false); }
+                else if (quant_from == kBF16) { if (dense) DARIC_MR(kMergeFromBF16, true); else DARIC_MR(kMergeFromBF16, false); }
+                else { if (dense) DARIC_MR(kMergeFromF16, true); else DARIC_MR(kMergeFromF16, false); }
 #undef DARIC_MR
-    } else {
-        const dim3 grid(static_cast<unsigned>((kmax + kMergeTok - 1) / kMergeTok),
-                        static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_layers));
-        const bool vec = (g.D * elem_size) % 16 == 0 && (g.sb * elem_size) % 16 == 0 &&
-                         (g.ss * elem_size) % 16 == 0 && (g.sh * elem_size) % 16 == 0 &&
-                         (g.v_off < 0 || (g.v_off * elem_size) % 16 == 0);
-        if (vec)
-            DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
-                         k_new, v_new, T, n_chunks, sel_idx, kmax);
-        else
-            DARIC_LAUNCH((merge_kernel<1>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
-                         k_new, v_new, T, n_chunks, sel_idx, kmax);
+            } else {
+                const dim3 grid(static_cast<unsigned>((kmax + kMergeTok - 1) / kMergeTok), static_cast<unsigned>(nc),
+                                static_cast<unsigned>(nl));
+                const bool vec = (g.D * elem_size) % 16 == 0 && (g.sb * elem_size) % 16 == 0 &&
+                                 (g.ss * elem_size) % 16 == 0 && (g.sh * elem_size) % 16 == 0 &&
+                                 (g.v_off < 0 || (g.v_off * elem_size) % 16 == 0);
+                if (vec)
+                    DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
+                                 k_new, v_new, T, n_chunks, sel_idx, kmax, c0, l0);
+                else
+                    DARIC_LAUNCH((merge_kernel<1>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
+                                 k_new, v_new, T, n_chunks, sel_idx, kmax, c0, l0);
+            }
+            check_launch("merge_rows");
+        }
     }
-    check_launch("merge_rows");
 }
 
 }  // namespace daric

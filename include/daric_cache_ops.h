@@ -159,7 +159,12 @@ int daric_copier_scatter_pages(daric_copier* copier, const char* const* layer_na
  * tails and tokens >= num_tokens[i] are copied unchanged. For an fp8 layer
  * the e4m3 codes are decoded, rotated in fp32 and re-encoded (saturating
  * round-to-nearest-even); a per-head scale would cancel, see
- * daric_copier_register_k_scale.
+ * daric_copier_register_k_scale. The one-pass kernel needs 16-byte aligned
+ * pages, strides and store offsets, K head rows dense in the page span and
+ * rotated halves that are 16-byte multiples; for any other layout accepted
+ * by the copy and rotation checks, the call scatters with the copy kernel and
+ * then rotates the moved tokens in place (pages with id 0 skipped by both),
+ * to the same results up to the rotation's rounding.
  * New entry point; no counterpart in the reference (which scatters in the
  * store process and rotates later in the worker process). */
 int daric_copier_scatter_pages_rerotate(daric_copier* copier,
@@ -182,7 +187,8 @@ int daric_copier_scatter_pages_rerotate(daric_copier* copier,
  * device array of 262144 bytes per GPU (3276 jobs of 80 bytes), carried there
  * by kernels whose arguments hold the bytes. It calls no hipMalloc, hipFree
  * or hipHostMalloc and enqueues only kernels. A call whose jobs need more
- * than the array holds returns DARIC_ERR_INVALID before any device work.
+ * than the array holds, or whose layout needs the scatter-then-rotate form,
+ * returns DARIC_ERR_INVALID before any device work.
  * Every call on one GPU uses that GPU's array, which keeps the last call's
  * descriptors: calls that overlap on one GPU (on different streams, or
  * graphs replayed concurrently) race on it, and the caller must order them. */
@@ -297,7 +303,9 @@ int daric_kv_deviation(const daric_tensor* layers, int64_t n_layers, int page_fi
 /* For every (layer, chunk) select the chunk's k tokens with the largest keys
  * (ties: lower token index first) and write their chunk-local token indices
  * in ascending order to out_idx[l, c, 0:k]; slots k..kmax-1 are set to -1.
- * keys: [n_layers, T] fp32; out_idx: [n_layers, n_chunks, kmax] int32. */
+ * keys: [n_layers, T] fp32; out_idx: [n_layers, n_chunks, kmax] int32.
+ * Chunks of any length: keys of chunks up to 8192 tokens are staged in LDS,
+ * longer chunks are read from global memory in each radix pass. */
 int daric_topk_per_chunk(const daric_tensor* keys, const daric_chunk* chunks,
                          int64_t n_chunks, daric_tensor* out_idx, uint64_t stream);
 

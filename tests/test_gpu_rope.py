@@ -132,15 +132,15 @@ def test_fused_large_spans_in_parts(dev, layout, dtype, neox):
                chunk_tokens=(128, 37, 40), deltas=(1024, -7168, 3))
 
 
-def test_fused_rejects_unaligned_rotary(dev):
-    t = torch.zeros(2, 4, 16, 2, 64, dtype=torch.bfloat16, device=dev)
-    gc = cache_ops.CacheCopier()
-    gc.register_layer("a", t, False)
-    gc.register_store(torch.zeros(2 * 16 * 2 * 64 * 2 * 2, dtype=torch.uint8, device=dev))
-    inv = torch.ones(12, device=dev)
-    with pytest.raises(RuntimeError, match="rotary pairs are not 16-byte aligned"):
-        gc.scatter_pages_rerotate(["a"], [0], [16384], torch.tensor([1, 2], dtype=torch.int32, device=dev),
-                                  [0, 2], [5], [32], inv, 24, True)
+@pytest.mark.parametrize("layout,dtype,neox,rotary_dim", [
+    ("nhd", torch.bfloat16, True, 24),     # NeoX halves of 12 elements: not 16-byte multiples
+    ("hnd", torch.float16, False, 20),     # GPT-J pairs over 40 bytes
+    ("pf", torch.uint8, True, 48),         # fp8 halves of 24 bytes
+])
+def test_fused_call_on_unaligned_rotary_scatters_then_rotates(dev, layout, dtype, neox, rotary_dim):
+    """Rotated halves that are not 16-byte multiples: the fused call scatters
+    and then rotates in place, to the oracle's bar."""
+    fused_case(dev, layout, dtype, neox, rotary_dim, seed=21)
 
 
 def inplace_case(dev, layout, dtype, neox, rotary_dim, nb=40, ps=16, h=4, d=64, L=3, seed=0):

@@ -223,3 +223,49 @@ def test_deviation_allocated_keys_on_a_side_stream(dev):
     want = osel.deviation(cpu, pf, bt, kn, moved)
     assert np.array_equal(keys.cpu().numpy().view(np.uint32), want.view(np.uint32))
     assert not keys[:, :10].any() and not keys[:, 10 + k_new.shape[1]:].any()
+
+
+def test_topk_chunk_longer_than_lds_budget(dev):
+    """A 20000-token chunk (past the 8192 tokens whose keys the kernel stages
+    in LDS) and a short one in the same call: the long chunk's keys are read
+    from global memory in every pass; indices bit-exact, ties to the lower
+    index (the keys repeat every 97 tokens)."""
+    rng = np.random.default_rng(11)
+    n_long, n_short = 20000, 300
+    base = rng.standard_normal(97).astype(np.float32) ** 2
+    keys = np.concatenate([np.tile(base, n_long // 97 + 1)[:n_long],
+                           rng.standard_normal(n_short).astype(np.float32) ** 2])[None, :].repeat(2, 0)
+    keys[1] = keys[1][::-1]
+    chunks = [(0, 0, n_long, 3001), (0, n_long, n_short, 45)]
+    want = osel.topk_per_chunk(keys, chunks, 3001)
+    got = cache_ops.topk_per_chunk(torch.from_numpy(keys.copy()).to(dev), chunks, kmax=3001)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), want)
+
+
+def test_selection_over_more_than_65535_chunks(dev):
+    """70000 chunks (past the 65535 a grid dimension holds): deviation, top-k
+    and merge cut their grids into slices; keys, indices and merged bytes
+    bit-exact against the oracle."""
+    g = torch.Generator().manual_seed(13)
+    n_chunks, ps, h, d = 70000, 1, 2, 64
+    nb = n_chunks + 8
+    layer = torch.randn(2, nb, ps, h, d, generator=g).to(torch.bfloat16)
+    # one-token chunks, each on a page of its own: every merged slot is distinct
+    bt = (torch.randperm(nb - 1, generator=g)[:n_chunks] + 1).numpy().astype(np.int32)
+    chunks = [(c, c, 1, 1) for c in range(n_chunks)]
+    k_new = torch.randn(1, n_chunks, h, d, generator=g).to(torch.bfloat16)
+    v_new = torch.randn(1, n_chunks, h, d, generator=g).to(torch.bfloat16)
+    gl = [layer.to(dev)]
+    btd = torch.from_numpy(bt).to(dev)
+    keys = cache_ops.kv_deviation(gl, False, btd, k_new.to(dev), chunks)
+    sel = cache_ops.topk_per_chunk(keys, chunks, kmax=1)
+    torch.cuda.synchronize()
+    keys_o = osel.deviation([layer], False, bt, k_new, chunks)
+    assert np.array_equal(keys.cpu().numpy().view(np.uint32), keys_o.view(np.uint32))
+    sel_o = osel.topk_per_chunk(keys_o, chunks, 1)
+    assert np.array_equal(sel.cpu().numpy(), sel_o)
+    cache_ops.merge_rows(gl, False, btd, k_new.to(dev), v_new.to(dev), chunks, sel)
+    torch.cuda.synchronize()
+    osel.merge_rows([layer], False, bt, k_new, v_new, chunks, sel_o)
+    assert same_bytes(gl[0], layer)
