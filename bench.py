@@ -621,6 +621,10 @@ def run_config5(steps, warmup, seed=0):
                                                          j["ioff"], j["deltas"], j["ntok"], w["inv"], D,
                                                          True, st), steps, warmup, stream)
     fused_bytes = T * L * 2 * (2 * H * D * 1)
+    # the same 1280 jobs as a plain scatter_pages (no rotation): this access
+    # pattern's copy rate on this box
+    pattern = time_steps(lambda: cp.scatter_pages(j["names"], j["offsets"], j["sizes"], w["idx"], j["ioff"], st),
+                         steps, 1, stream)
     # selection on the fp8 cache: recomputed K (bf16) vs the dequantised cached
     # K, top-10%, then the selected bf16 K/V rows quantised into the cache
     bt, chunks, k_new, v_new = w["bt"], w["chunks"], w["k_new"], w["v_new"]
@@ -655,6 +659,9 @@ def run_config5(steps, warmup, seed=0):
                kernel_ms=fused["kern_ms"], algorithmic_bytes=fused_bytes,
                GBps=_gbps(fused_bytes, fused["kern_ms"]),
                frac=_gbps(fused_bytes, fused["kern_ms"]) / PEAK_HBM_GBPS,
+               pattern_copy=dict(kernel="copy_pages_kernel<16,scatter> on the same 1280 jobs, no rotation",
+                                 kernel_ms=pattern["kern_ms"], GBps=_gbps(fused_bytes, pattern["kern_ms"]),
+                                 fused_frac_of_it=pattern["kern_ms"] / fused["kern_ms"]),
                selection=dict(k=k, ms_per_step=selection["step_ms"], algorithmic_bytes=sel_bytes,
                               GBps=_gbps(sel_bytes, selection["step_ms"]),
                               kernels={"deviation": dict(ms=parts["deviation"], bytes=dev_bytes,
