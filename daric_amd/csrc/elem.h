@@ -92,6 +92,39 @@ __device__ inline uint32_t f32x4_to_e4m3_hw(const float* v) {
 #endif
 }
 
+// ---- x / scale for quantising writes ---------------------------------------
+// A cache write quantises x as e4m3(x / scale), the quotient correctly rounded
+// to fp32. For scales in [2^-60, 2^60] one correctly rounded reciprocal per
+// scale replaces the per-element division: q0 = x * r, the remainder
+// x - q0 * scale exactly by one FMA, and one correction q0 + rem * r by a
+// second (Markstein's correction step). That gives the correctly rounded
+// quotient wherever the code depends on it, and a quotient that saturates the
+// same way where it does not (checked for every bf16 and fp16 x against a set
+// of scales by the CPU tests). Other scales, NaN among them, divide.
+struct QuantDiv {
+    float s, r;
+    bool fast;
+};
+__host__ __device__ inline QuantDiv quant_div(float s) {
+    QuantDiv d;
+    d.s = s;
+    d.r = 1.0f / s;
+    d.fast = s >= 0x1p-60f && s <= 0x1p60f;
+    return d;
+}
+// The quotient for a scale with d.fast set.
+__host__ __device__ inline float quant_quotient_fast(const QuantDiv& d, float x) {
+    const float q0 = x * d.r;
+    const float rem = __builtin_fmaf(-q0, d.s, x);
+    const float q1 = __builtin_fmaf(rem, d.r, q0);
+    // x infinite or NaN, or the quotient overflowed: q0. The sign is x's (the
+    // correction of x = -0 sums +0 and -0).
+    return __builtin_isfinite(q0) ? __builtin_copysignf(q1, x) : q0;
+}
+__host__ __device__ inline float quant_quotient(const QuantDiv& d, float x) {
+    return d.fast ? quant_quotient_fast(d, x) : x / d.s;
+}
+
 // ---- 16-byte vector <-> fp32 lanes ----------------------------------------
 // Kind codes used as template parameters.
 enum ElemKind : int { kBF16 = 0, kF16 = 1, kE4M3 = 2 };

@@ -21,6 +21,15 @@ void daric_hosttest_encode_bf16(const float* in, uint16_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = static_cast<uint16_t>(daric::f32_to_bf16(in[i]));
 }
 
+// out[i * n_x + j] = the quantising writes' quotient of x[j] by scales[i].
+void daric_hosttest_quant_quotients(const float* x, int64_t n_x, const float* scales, int64_t n_s,
+                                    float* out) {
+    for (int64_t i = 0; i < n_s; ++i) {
+        const daric::QuantDiv d = daric::quant_div(scales[i]);
+        for (int64_t j = 0; j < n_x; ++j) out[i * n_x + j] = daric::quant_quotient(d, x[j]);
+    }
+}
+
 // Returns the number of n in [n0, n1) for which FastDiv(d).div(n) != n / d.
 int64_t daric_hosttest_fastdiv_errors(uint32_t d, uint32_t n0, uint32_t n1) {
     const daric::FastDiv f(d);

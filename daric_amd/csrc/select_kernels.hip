@@ -343,7 +343,8 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(
 // MODE 0 copies bytes (rows and cache share their element type). MODE kBF16 /
 // kF16 + 1 quantises bf16 / fp16 rows into an e4m3 cache as vLLM's fp8 cache
 // write does: code = saturating RTNE of float32(x) / scale[l, h], the
-// division correctly rounded.
+// division correctly rounded (quant_quotient: one reciprocal per 16-byte unit
+// and two FMAs per element instead of a division per element).
 constexpr int kMergeUnits = 8;
 // 256 lanes x 8 units in flight. A same-process sweep at config 3 put 128 or
 // 512 lanes, 4 or 16 units, nontemporal loads or stores, a precomputed slot
@@ -429,12 +430,17 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
         if constexpr (MODE == kMergeCopy) {
             *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(un) * 16) = v[s];
         } else {
-            const float sc = (kv ? v_scales : k_scales)[l * g.H + h];
+            const QuantDiv qd = quant_div((kv ? v_scales : k_scales)[l * g.H + h]);
             float x[8];
 #pragma unroll
             for (int w = 0; w < 4; ++w) Elem<MODE - 1>::unpack_word(v[s][w], x + 2 * w);
+            if (qd.fast) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) x[i] = x[i] / sc;
+                for (int i = 0; i < 8; ++i) x[i] = quant_quotient_fast(qd, x[i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[i] = x[i] / qd.s;
+            }
             u32x2 o;
             o[0] = f32x4_to_e4m3_hw(x);
             o[1] = f32x4_to_e4m3_hw(x + 4);

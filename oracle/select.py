@@ -144,7 +144,8 @@ def quantise_rows(rows: torch.Tensor, scales) -> torch.Tensor:
     rows (daric/integration/vllm/worker.py:336-345, utils.py:406-427)."""
     x = rows.to(torch.float32).numpy()
     s = np.asarray(scales, np.float32).reshape(-1, 1)
-    q = (x / s).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):   # saturating cases
+        q = (x / s).astype(np.float32)
     return torch.from_numpy(fp8.encode(q)).view(rows.shape)
 
 

@@ -45,6 +45,8 @@ def hosttest(lib):
     h.daric_hosttest_f32_to_f16.restype = ctypes.c_uint32
     h.daric_hosttest_fastdiv_errors.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
     h.daric_hosttest_fastdiv_errors.restype = ctypes.c_int64
+    h.daric_hosttest_quant_quotients.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                                 ctypes.c_int64, ctypes.c_void_p]
     return h
 
 
@@ -310,6 +312,50 @@ def test_host_fp8_conversion_matches_oracle(hosttest):
         got = hosttest.daric_hosttest_e4m3_to_f32(c)
         ref = float(ofp8.decode([c])[0])
         assert (np.isnan(got) and np.isnan(ref)) or got == ref
+
+
+def test_quant_quotient_is_correctly_rounded_division(hosttest):
+    """The quantising merge's x / scale (one reciprocal per scale and two FMAs
+    per element for scales in [2^-60, 2^60], a division otherwise) against
+    numpy's IEEE float32 division, for every bf16 and every fp16 value of x
+    (zeros, subnormals, infinities and NaNs included) and 320 scales: random
+    ones over the whole fast range and over typical fp8 scales, significands of
+    all ones and of 1 + a few ulps (where a reciprocal rounds worst), powers of
+    two, and scales outside the fast range. The float32 quotient must be the
+    correctly rounded one wherever |x / scale| lies in [2^-11, 480] (the e4m3
+    codes depend on its bits only there), and the e4m3 code must be equal for
+    every x."""
+    bits = np.arange(65536, dtype=np.uint32)
+    x = np.ascontiguousarray(np.concatenate([
+        (bits << 16).view(np.float32),
+        bits.astype(np.uint16).view(np.float16).astype(np.float32)]))
+    rng = np.random.default_rng(11)
+    n = 40
+    scales = np.concatenate([
+        np.exp2(rng.uniform(-60, 60, n)),
+        np.exp(rng.uniform(np.log(1e-5), np.log(1e3), n)),
+        np.float32(2 - 2.0 ** -23) * np.exp2(rng.integers(-40, 40, n).astype(np.float64)),
+        (np.uint32(0x3f800000) + rng.integers(1, 16, n).astype(np.uint32)).view(np.float32)
+        * np.exp2(rng.integers(-30, 30, n).astype(np.float64)),
+        (np.uint32(0x3fffffff) - rng.integers(0, 16, n).astype(np.uint32)).view(np.float32)
+        * np.exp2(rng.integers(-30, 30, n).astype(np.float64)),
+        np.exp2(rng.integers(-60, 61, n).astype(np.float64)),
+        np.array([2.0 ** -60, 2.0 ** 60, 2.0 ** -61, 2.0 ** 61, 2.0 ** -70, 2.0 ** 70, 1e-30, 1e30,
+                  0.0017, 0.25, 1.0, 3.0, 448.0, 0.007, 1.1754944e-38, 3.0e38] * (n // 16)),
+        np.exp2(rng.uniform(-80, 80, n)),
+    ]).astype(np.float32)
+    scales = np.ascontiguousarray(scales)
+    for i in range(0, len(scales), 32):
+        sc = np.ascontiguousarray(scales[i:i + 32])
+        got = np.empty((len(sc), len(x)), np.float32)
+        hosttest.daric_hosttest_quant_quotients(x.ctypes.data, len(x), sc.ctypes.data, len(sc),
+                                                got.ctypes.data)
+        with np.errstate(all="ignore"):
+            want = (x[None, :] / sc[:, None]).astype(np.float32)
+            region = (np.abs(want) >= 2.0 ** -11) & (np.abs(want) <= 480)
+        bad = region & (got.view(np.uint32) != want.view(np.uint32))
+        assert not bad.any(), (sc[np.nonzero(bad)[0][0]], x[np.nonzero(bad)[1][0]])
+        assert np.array_equal(ofp8.encode(got.ravel()), ofp8.encode(want.ravel()))
 
 
 def test_host_bf16_f16_conversion_matches_torch(hosttest):

@@ -83,8 +83,15 @@ def test_quantising_merge_parity(dev, layout, row_dtype):
     k_new = (torch.randn(L, T, H, D, generator=g) * 5).to(row_dtype)
     v_new = (torch.randn(L, T, H, D, generator=g) * 5).to(row_dtype)
     k_new[0, 0, 0, :4] = torch.tensor([1e4, -1e4, 0.0, -0.0])        # saturation and signed zero
+    k_new[0, 0, 0, 4:8] = torch.tensor([float("inf"), -float("inf"), 1e-39, 3e38]).to(row_dtype)
     ks = (0.004 + 0.03 * torch.rand(L, H, generator=g)).float()
     vs = (0.004 + 0.03 * torch.rand(L, H, generator=g)).float()
+    # scales outside [2^-60, 2^60] take the kernel's dividing path: rows scaled
+    # alike keep bf16 codes in range (fp16 rows saturate or vanish)
+    hv = min(1, H - 1)
+    ks[1, 0] = 2.0 ** -70
+    vs[2, hv] = 2.0 ** 62
+    v_new[2, :, hv] = (v_new[2, :, hv].float() * 2.0 ** 62).to(row_dtype)
     kmax = max(c[3] for c in chunks)
     sel = np.full((L, len(chunks), kmax), -1, np.int32)
     rng = np.random.default_rng(5)
