@@ -116,20 +116,6 @@ def time_steps(step, steps, warmup, stream):
                 launches_per_step=launches / max(steps, 1))
 
 
-def _event_ms(fn, steps, stream, warmup=2):
-    """Milliseconds per call of fn (HIP events around `steps` back-to-back calls)."""
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        fn()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
-
-
 def run_gpu(cfg, steps, warmup):
     from daric_amd import cache_ops
     dev = torch.device("cuda:0")
@@ -295,13 +281,26 @@ def run_config3(steps, warmup, seed=0):
     seq_sel = torch.arange(k, dtype=torch.int32, device=dev).repeat(L, n_chunk, 1).contiguous()
     seq_ms = time_steps(lambda: cache_ops.merge_rows(layers, False, seq_bt, k_new, v_new, chunks, seq_sel,
                                                      stream=st), steps, 1, stream)["kern_ms"]
-    # and a contiguous device copy of the same byte count (torch copy_): the
-    # streaming ceiling the merge is held against
-    half_bytes = len(chunks) * k * L * (2 * H * D * 2)
-    flat_src = torch.empty(half_bytes, dtype=torch.uint8, device=dev)
-    flat_dst = torch.empty_like(flat_src)
-    flat_ms = _event_ms(lambda: flat_dst.copy_(flat_src), steps, stream)
-    del flat_src, flat_dst
+    # and the library's page scatter moving the same byte count from a
+    # contiguous staging buffer onto random pages of the same cache layers:
+    # the same access pattern with 32 KiB page spans for 2 KiB rows
+    span = PS * H * D * 2
+    npg = (n_chunk * k * (2 * H * D * 2)) // (2 * span)            # pages per layer
+    staging = torch.empty(L * npg * 2 * span, dtype=torch.uint8, device=dev)
+    cp = cache_ops.CacheCopier()
+    names = [f"merge_ref.{i}" for i in range(L)]
+    for n, t in zip(names, layers):
+        cp.register_layer(n, t, False)
+    cp.register_store(staging)
+    gen = torch.Generator().manual_seed(seed + 7)
+    NB = layers[0].shape[1]
+    page_ids = torch.cat([torch.randperm(NB - 1, generator=gen)[:npg] + 1 for _ in range(L)]).to(torch.int32).to(dev)
+    sc_offs = [i * npg * 2 * span for i in range(L)]
+    sc_ioff = [i * npg for i in range(L + 1)]
+    sc_ms = time_steps(lambda: cp.scatter_pages(names, sc_offs, [npg * 2 * span] * L, page_ids, sc_ioff, st),
+                       steps, 1, stream)["kern_ms"]
+    sc_bytes = 2 * L * npg * 2 * span
+    del cp, staging
     e = 2
     dev_bytes = T * L * (2 * H * D * e) + T * L * 4
     topk_bytes = T * L * 4 + n_chunk * L * k * 4
@@ -323,11 +322,12 @@ def run_config3(steps, warmup, seed=0):
                                           note="the same merge_rows kernel and byte count with every "
                                                "chunk's first k tokens on consecutive blocks: sequential "
                                                "2 KiB rows on both sides"),
-                                      contiguous_copy=dict(
-                                          ms=flat_ms, GBps=_gbps(merge_bytes, flat_ms),
-                                          merge_frac_of_it=flat_ms / parts["merge"],
-                                          note="torch copy_ of the same byte count between two contiguous "
-                                               "device buffers, same process"))})
+                                      page_scatter=dict(
+                                          ms=sc_ms, bytes=sc_bytes, GBps=_gbps(sc_bytes, sc_ms),
+                                          merge_frac_of_it=_gbps(merge_bytes, parts["merge"]) / _gbps(sc_bytes, sc_ms),
+                                          note="scatter_pages of about the same byte count from a contiguous "
+                                               "staging buffer onto random 32 KiB page spans of the same cache "
+                                               "layers, same process"))})
     del w, layers, k_new, v_new, keys, sel
     torch.cuda.empty_cache()
     return out
