@@ -164,7 +164,9 @@ int daric_copier_scatter_pages(daric_copier* copier, const char* const* layer_na
  * rotated halves that are 16-byte multiples; for any other layout accepted
  * by the copy and rotation checks, the call scatters with the copy kernel and
  * then rotates the moved tokens in place (pages with id 0 skipped by both),
- * to the same results up to the rotation's rounding.
+ * to the same results up to the rotation's rounding. (A page listed by two
+ * jobs of one call is written twice, a race on either path; on the two-pass
+ * path it is also rotated once per listing.)
  * New entry point; no counterpart in the reference (which scatters in the
  * store process and rotates later in the worker process). */
 int daric_copier_scatter_pages_rerotate(daric_copier* copier,
