@@ -346,11 +346,12 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(
 // division correctly rounded (quant_quotient: one reciprocal per 16-byte unit
 // and two FMAs per element instead of a division per element).
 constexpr int kMergeUnits = 8;
-// 256 lanes x 8 units in flight. A same-process sweep at config 3 put 128 or
-// 512 lanes, 4 or 16 units, nontemporal loads or stores, a precomputed slot
-// table, two groups per workgroup and one-wavefront-per-token forms all
-// within +-2% of this, and the whole merge within 8-10% of a contiguous
-// copy of the same bytes.
+// 256 lanes x 8 units in flight, nontemporal loads (and stores of copied
+// rows): 2% faster for the copy and 4-5% for the quantising merge than plain
+// accesses, in alternating processes. A same-process sweep at config 3 put 128
+// or 512 lanes, 1 to 16 units, a precomputed slot table, two groups per
+// workgroup and one-wavefront-per-token forms within +-2% of this, and the
+// merge at about 90% of a page scatter of the same bytes.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeMaxTok = 64;
 constexpr int kMergeCopy = 0;
@@ -405,7 +406,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
         const int kv = r >= units ? 1 : 0;
         const int64_t src = s_src[t];
         const uint8_t* p = src >= 0 ? (kv ? v_new : k_new) + src + static_cast<int64_t>(r - kv * units) * 16 : k_new;
-        v[s] = *reinterpret_cast<const u32x4*>(p);
+        v[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     }
     uint8_t* __restrict__ base = layers[l];
     const int upr = static_cast<int>(d_upr.d);
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
         const int un = DENSE ? u : u - h * upr;
         uint8_t* dst = base + s_dst[t] + (static_cast<int64_t>(DENSE ? 0 : h) * g.sh + (kv ? g.v_off : 0)) * ces;
         if constexpr (MODE == kMergeCopy) {
-            *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(un) * 16) = v[s];
+            __builtin_nontemporal_store(v[s], reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(un) * 16));
         } else {
             const QuantDiv qd = quant_div((kv ? v_scales : k_scales)[l * g.H + h]);
             float x[8];
