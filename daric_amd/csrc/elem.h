@@ -66,8 +66,10 @@ __host__ __device__ inline uint32_t f32_to_e4m3(float f) {
 
 // gfx950 conversion instructions (v_cvt_pk_f32_fp8 / v_cvt_pk_fp8_f32, OCP
 // e4m3 on this target). The encoder clamps to +-448 first, so the result is
-// the saturating RTNE code for every finite input. The host pass (never
-// executed) falls back to the scalar functions.
+// the saturating RTNE code for every finite input and infinity; NaN inputs
+// get the NaN code of their sign (gfx950's conversion: NaN -> 0xff, +inf ->
+// 0x7f, -inf -> 0xff). The host pass (never executed) falls back to the
+// scalar functions.
 __device__ inline void e4m3x4_to_f32_hw(uint32_t w, float* out) {
 #ifdef __HIP_DEVICE_COMPILE__
     auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
@@ -79,13 +81,17 @@ __device__ inline void e4m3x4_to_f32_hw(uint32_t w, float* out) {
 }
 __device__ inline uint32_t f32x4_to_e4m3_hw(const float* v) {
 #ifdef __HIP_DEVICE_COMPILE__
-    const float c0 = __builtin_amdgcn_fmed3f(v[0], -448.0f, 448.0f);
-    const float c1 = __builtin_amdgcn_fmed3f(v[1], -448.0f, 448.0f);
-    const float c2 = __builtin_amdgcn_fmed3f(v[2], -448.0f, 448.0f);
-    const float c3 = __builtin_amdgcn_fmed3f(v[3], -448.0f, 448.0f);
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(c0, c1, 0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(c2, c3, w, true);
-    return (uint32_t)w;
+    // The clamp would turn a NaN into a finite value, and the conversion gives
+    // every NaN the code 0xff; an infinity of the NaN's sign converts to the
+    // NaN code of that sign (0x7f or 0xff), as f32_to_e4m3 encodes NaN.
+    float c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        c[i] = v[i] != v[i] ? __builtin_copysignf(__builtin_huge_valf(), v[i])
+                            : __builtin_amdgcn_fmed3f(v[i], -448.0f, 448.0f);
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], w, true);
+    return static_cast<uint32_t>(w);
 #else
     return f32_to_e4m3(v[0]) | (f32_to_e4m3(v[1]) << 8) | (f32_to_e4m3(v[2]) << 16) |
            (f32_to_e4m3(v[3]) << 24);

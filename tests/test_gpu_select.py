@@ -84,6 +84,7 @@ def test_quantising_merge_parity(dev, layout, row_dtype):
     v_new = (torch.randn(L, T, H, D, generator=g) * 5).to(row_dtype)
     k_new[0, 0, 0, :4] = torch.tensor([1e4, -1e4, 0.0, -0.0])        # saturation and signed zero
     k_new[0, 0, 0, 4:8] = torch.tensor([float("inf"), -float("inf"), 1e-39, 3e38]).to(row_dtype)
+    k_new[0, 0, 0, 8:10] = torch.tensor([float("nan"), -float("nan")]).to(row_dtype)   # NaN codes keep the sign
     ks = (0.004 + 0.03 * torch.rand(L, H, generator=g)).float()
     vs = (0.004 + 0.03 * torch.rand(L, H, generator=g)).float()
     # scales outside [2^-60, 2^60] take the kernel's dividing path: rows scaled
