@@ -121,11 +121,11 @@ __host__ __device__ inline QuantDiv quant_div(float s) {
 // The quotient for a scale with d.fast set.
 __host__ __device__ inline float quant_quotient_fast(const QuantDiv& d, float x) {
     const float q0 = x * d.r;
-    const float rem = __builtin_fmaf(-q0, d.s, x);
-    const float q1 = __builtin_fmaf(rem, d.r, q0);
-    // x infinite or NaN, or the quotient overflowed: q0. The sign is x's (the
-    // correction of x = -0 sums +0 and -0).
-    return __builtin_isfinite(q0) ? __builtin_copysignf(q1, x) : q0;
+    // the negated remainder q0 * scale - x, so that x = -0 ends as
+    // -0 + -0 = -0 (with x - q0 * scale it would end as +0)
+    const float nrem = __builtin_fmaf(q0, d.s, -x);
+    const float q1 = __builtin_fmaf(-nrem, d.r, q0);
+    return __builtin_isfinite(q0) ? q1 : q0;   // x infinite or NaN, or the quotient overflowed
 }
 __host__ __device__ inline float quant_quotient(const QuantDiv& d, float x) {
     return d.fast ? quant_quotient_fast(d, x) : x / d.s;
