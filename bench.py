@@ -174,11 +174,18 @@ def run_gpu(cfg, steps, warmup):
 
     inplace = time_steps(rstep, steps, warmup, stream)
     inplace_bytes = sum(s[2] for s in segs) * L * cfg["kv_heads"] * cfg["head_dim"] * 2 * 2
+
+    # the same call on consecutive pages (blocks 1..512): the kernel's rate
+    # without the block table's random page addresses
+    bt_seq = torch.arange(1, bt_all.numel() + 1, dtype=torch.int32, device=dev)
+    inplace_seq = time_steps(lambda: cache_ops.rerotate_pages(w["cache"], False, bt_seq, segs, inv,
+                                                              cfg["head_dim"], True, stream=stream.cuda_stream),
+                             steps, 1, stream)
     return dict(step_ms=fused["step_ms"], wall_s=fused["wall_s"], kern_ms=fused["kern_ms"],
                 p_kern_ms=plain["kern_ms"],
                 g_step_ms=gather["step_ms"], g_kern_ms=gather["kern_ms"], T=T, L=L,
                 r_step_ms=inplace["step_ms"], r_kern_ms=inplace["kern_ms"], r_bytes=inplace_bytes,
-                r_tokens=sum(s[2] for s in segs))
+                r_seq_kern_ms=inplace_seq["kern_ms"], r_tokens=sum(s[2] for s in segs))
 
 
 # ---------------------------------------------------------------------------
@@ -856,6 +863,9 @@ def main():
                              "GBps": _gbps(r["r_bytes"], r["r_kern_ms"]),
                              "frac": _gbps(r["r_bytes"], r["r_kern_ms"]) / PEAK_HBM_GBPS,
                              "tokens_per_s": r["r_tokens"] / (r["r_step_ms"] / 1e3),
+                             "sequential_pages": {"kernel_ms": r["r_seq_kern_ms"],
+                                                  "GBps": _gbps(r["r_bytes"], r["r_seq_kern_ms"]),
+                                                  "note": "the same call with the pages on blocks 1..512"},
                              "note": "rerotate_pages of chunks 1..7 (chunk 0 does not move) in all "
                                      "layers: K rotated elements read and written"},
         "extra": extra,
