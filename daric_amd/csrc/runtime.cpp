@@ -88,59 +88,64 @@ DescRing& DescRing::for_device(int device) {
 }
 
 void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* slot_out, bool direct) {
-    std::unique_lock<std::mutex> lk(mu_);
     // A slot between upload() and release() belongs to a call that is still
-    // enqueueing kernels on it; skip such slots (wait if all are taken).
+    // enqueueing kernels on it; skip such slots (wait if all are taken). The
+    // lock covers only the choice of the slot: waiting for its previous
+    // kernels and filling it happen outside, so that other threads can take
+    // slots meanwhile.
     int idx = -1;
-    for (;;) {
-        for (int k = 0; k < kSlots; ++k) {
-            const int c = (next_ + k) % kSlots;
-            if (!slots_[c].in_use) { idx = c; break; }
-        }
-        if (idx >= 0) break;
-        lk.unlock();
-        std::this_thread::yield();
-        lk.lock();
-    }
-    next_ = (idx + 1) % kSlots;
-    // All slots get kInitialCap bytes at the ring's first use: growing a slot
-    // later frees device memory (hipFree waits for the device), which would
-    // stall a call in the middle of a pipelined stream of calls. 1 MiB holds
-    // the descriptors of ~13000 copy jobs.
-    if (!initialised_) {
-        for (Slot& t : slots_) {
-            if (t.ev == nullptr) DARIC_HIP_CHECK(hipEventCreateWithFlags(&t.ev, hipEventDisableTiming));
-            if (t.cap == 0) {
-                DARIC_HIP_CHECK(hipHostMalloc(&t.host, kInitialCap, hipHostMallocCoherent));
-                DARIC_HIP_CHECK(hipMalloc(&t.dev, kInitialCap));
-                t.cap = kInitialCap;
+    {
+        std::unique_lock<std::mutex> lk(mu_);
+        for (;;) {
+            for (int k = 0; k < kSlots; ++k) {
+                const int c = (next_ + k) % kSlots;
+                if (!slots_[c].in_use) { idx = c; break; }
             }
+            if (idx >= 0) break;
+            lk.unlock();
+            std::this_thread::yield();
+            lk.lock();
         }
-        initialised_ = true;
+        // All slots get kInitialCap bytes at the ring's first use: growing a
+        // slot later frees device memory (hipFree waits for the device), which
+        // would stall a call in the middle of a pipelined stream of calls.
+        // 1 MiB holds the descriptors of ~13000 copy jobs.
+        if (!initialised_) {
+            for (Slot& t : slots_) {
+                if (t.ev == nullptr) DARIC_HIP_CHECK(hipEventCreateWithFlags(&t.ev, hipEventDisableTiming));
+                if (t.cap == 0) {
+                    DARIC_HIP_CHECK(hipHostMalloc(&t.host, kInitialCap, hipHostMallocCoherent));
+                    DARIC_HIP_CHECK(hipMalloc(&t.dev, kInitialCap));
+                    t.cap = kInitialCap;
+                }
+            }
+            initialised_ = true;
+        }
+        next_ = (idx + 1) % kSlots;
+        slots_[idx].in_use = true;
     }
     Slot& s = slots_[idx];
-    s.in_use = true;
-    if (s.pending) {
-        DARIC_HIP_CHECK(hipEventSynchronize(s.ev));
-        s.pending = false;
-    }
-    if (bytes > s.cap) {
-        size_t cap = s.cap * 2;
-        while (cap < bytes) cap *= 2;
-        if (s.host) DARIC_HIP_CHECK(hipHostFree(s.host));
-        if (s.dev) DARIC_HIP_CHECK(hipFree(s.dev));
-        s.host = nullptr;
-        s.dev = nullptr;
-        s.cap = 0;
-        // Coherent (fine-grained) pinned memory: the upload kernel reads it
-        // over the bus, so no stale GPU-cached copy of an earlier use of the
-        // slot can be seen.
-        DARIC_HIP_CHECK(hipHostMalloc(&s.host, cap, hipHostMallocCoherent));
-        DARIC_HIP_CHECK(hipMalloc(&s.dev, cap));
-        s.cap = cap;
-    }
     *slot_out = idx;
     try {
+        if (s.pending) {
+            DARIC_HIP_CHECK(hipEventSynchronize(s.ev));
+            s.pending = false;
+        }
+        if (bytes > s.cap) {
+            size_t cap = s.cap * 2;
+            while (cap < bytes) cap *= 2;
+            if (s.host) DARIC_HIP_CHECK(hipHostFree(s.host));
+            if (s.dev) DARIC_HIP_CHECK(hipFree(s.dev));
+            s.host = nullptr;
+            s.dev = nullptr;
+            s.cap = 0;
+            // Coherent (fine-grained) pinned memory: the upload kernel reads it
+            // over the bus, so no stale GPU-cached copy of an earlier use of the
+            // slot can be seen.
+            DARIC_HIP_CHECK(hipHostMalloc(&s.host, cap, hipHostMallocCoherent));
+            DARIC_HIP_CHECK(hipMalloc(&s.dev, cap));
+            s.cap = cap;
+        }
         std::memcpy(s.host, src, bytes);
         // Direct: the kernels read the coherent pinned slot themselves; the
         // event recorded at release() keeps the slot until they are done.
@@ -152,6 +157,7 @@ void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* s
         // multiples of at least 1 MiB, so the rounded copy stays in bounds.
         launch_upload(s.host, s.dev, (bytes + 15) / 16, stream);
     } catch (...) {
+        std::lock_guard<std::mutex> lk(mu_);
         s.in_use = false;
         throw;
     }

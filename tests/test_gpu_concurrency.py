@@ -75,3 +75,80 @@ def test_threads_streams_and_copiers(dev):
         assert torch.equal(got_stage, stage), f"thread {tid} staging differs"
         for a, b in zip(got_cache, cache):
             assert same_bytes(a, b), f"thread {tid} cache differs"
+
+
+def test_sixteen_threads_share_the_descriptor_ring(dev):
+    """16 threads, as the store's RPC workers, each with its own copiers and
+    stream, issue calls of 48 jobs: too many descriptors for the kernel
+    arguments, so every call takes one of the ring's 16 slots. Each thread runs
+    a fused scatter + re-rotation of its own pages and a gather of them back,
+    8 rounds, gathering round r into its own region; every region must equal
+    what the same two calls gave when run alone beforehand."""
+    L, NB, PS, H, D = 4, 1024, 16, 4, 64
+    n_threads, rounds, chunks, ppc = 16, 8, 12, 4
+    span = PS * H * D * 2
+    job = 2 * ppc * span
+    n_jobs = chunks * L
+    g = torch.Generator(device=dev).manual_seed(3)
+    layers = [torch.randn(2, NB, PS, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(L)]
+    names = [f"layer.{l}" for l in range(L)]
+    inv = (1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))).to(dev)
+
+    def setup(t):
+        pages = [1 + t * chunks * ppc + i for i in range(chunks * ppc)]
+        flat, ioff, deltas, ntok = [], [0], [], []
+        for c in range(chunks):
+            for _ in range(L):
+                flat.extend(pages[c * ppc:(c + 1) * ppc])
+                ioff.append(len(flat))
+                deltas.append(c * ppc * PS + 1 + t)
+                ntok.append(ppc * PS - t % 3)
+        staging = torch.randn(n_jobs * job // 2, generator=g, device=dev).to(torch.bfloat16).view(torch.uint8)
+        out = torch.zeros(rounds * n_jobs * job, dtype=torch.uint8, device=dev)
+        wcp, rcp = cache_ops.CacheCopier(), cache_ops.CacheCopier()
+        for n, lt in zip(names * 1, layers):
+            wcp.register_layer(n, lt, False)
+            rcp.register_layer(n, lt, False)
+        wcp.register_store(staging)
+        rcp.register_store(out)
+        jn = [names[i % L] for i in range(n_jobs)]
+        offs = [i * job for i in range(n_jobs)]
+        idx = torch.tensor(flat, dtype=torch.int32, device=dev)
+        return dict(wcp=wcp, rcp=rcp, jn=jn, offs=offs, idx=idx, ioff=ioff, deltas=deltas, ntok=ntok,
+                    staging=staging, out=out)
+
+    def run(s, r, st):
+        s["wcp"].scatter_pages_rerotate(s["jn"], s["offs"], [job] * n_jobs, s["idx"], s["ioff"], s["deltas"],
+                                        s["ntok"], inv, D, True, st)
+        s["rcp"].gather_pages(s["jn"], [r * n_jobs * job + o for o in s["offs"]], [job] * n_jobs, s["idx"],
+                              s["ioff"], st)
+
+    work = [setup(t) for t in range(n_threads)]
+    expected = []
+    for s in work:
+        run(s, 0, torch.cuda.current_stream(dev).cuda_stream)
+        torch.cuda.synchronize()
+        expected.append(s["out"][: n_jobs * job].clone())
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(t):
+        try:
+            st = torch.cuda.Stream(device=dev)
+            st.wait_stream(torch.cuda.current_stream(dev))
+            for r in range(rounds):
+                run(work[t], r, st.cuda_stream)
+            st.synchronize()
+        except Exception as e:  # surfaced below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(n_threads)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    for t, s in enumerate(work):
+        got = s["out"].view(rounds, n_jobs * job)
+        for r in range(rounds):
+            assert torch.equal(got[r], expected[t]), f"thread {t} round {r}"
