@@ -340,6 +340,47 @@ def run_config3(steps, warmup, seed=0):
     return out
 
 
+def run_placement(steps, warmup, seed=0):
+    """The headline fused call on two config-2 caches held at once (the same
+    seeded contents and block table, allocated one after the other), timed
+    alternately: how much the cache's place in memory moves the kernel.
+    Opt-in (--extra place): the two caches take 258 GiB."""
+    from daric_amd import cache_ops
+    dev = torch.device("cuda:0")
+    cfg = CFG2
+    stream = torch.cuda.current_stream(dev)
+    calls = []
+    for _ in range(2):
+        w = build_workload(cfg, dev, seed=seed)
+        cp = cache_ops.CacheCopier()
+        for name, t in zip(w["names"], w["cache"]):
+            cp.register_layer(name, t, False)
+        cp.register_store(w["staging"])
+        j = w["jobs"]
+        idx = torch.tensor(j["flat"], dtype=torch.int32, device=dev)
+        inv = w["inv_freq"].to(dev)
+        calls.append((w, cp, idx, inv, j))
+
+    def step_of(c):
+        w, cp, idx, inv, j = c
+        return lambda: cp.scatter_pages_rerotate(j["names"], j["offsets"], j["sizes"], idx, j["ioff"],
+                                                 j["deltas"], j["ntok"], inv, cfg["head_dim"], True,
+                                                 stream.cuda_stream)
+    times = [[], []]
+    for _ in range(3):
+        for k in (0, 1):
+            times[k].append(time_steps(step_of(calls[k]), steps, warmup, stream)["kern_ms"])
+    nbytes = algorithmic_bytes(cfg)
+    out = {f"cache_{k}": dict(kernel_ms=times[k], GBps=[_gbps(nbytes, t) for t in times[k]],
+                              cache_address=hex(calls[k][0]["cache"][0].data_ptr()))
+           for k in (0, 1)}
+    out["note"] = ("the headline fused call on two caches allocated one after the other and held at "
+                   "once, timed alternately three times each")
+    del calls
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_config2_hnd(steps, warmup, seed=0):
     """Config 2's return path on a head-major cache: the request's 8 x 1024
     tokens in 32 layers of a [2, 65536, 16, 8, 128] bf16 cache stored HND
@@ -807,7 +848,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--extra", default="2h,3,4,5",
-                    help="other BASELINE configs to measure after the headline (comma list, or 'none')")
+                    help="other BASELINE configs to measure after the headline (comma list of 2h, 3, 4, "
+                         "5, or 'none'; 'place' adds the cache-placement check, 258 GiB)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (torch copy_) `steps` times, the "
                          "known-size reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -827,9 +869,11 @@ def main():
     g_achieved = nbytes / (r["g_kern_ms"] / 1e3) / 1e9
     torch.cuda.empty_cache()
     extra = {}
-    runners = {"2h": run_config2_hnd, "3": run_config3, "4": run_config4, "5": run_config5}
+    runners = {"2h": run_config2_hnd, "3": run_config3, "4": run_config4, "5": run_config5,
+               "place": run_placement}
     for cname in [x.strip() for x in a.extra.split(",") if x.strip() and x.strip() != "none"]:
-        extra[f"config{cname}"] = runners[cname](max(3, a.steps // 2), max(1, a.warmup))
+        key = "placement" if cname == "place" else f"config{cname}"
+        extra[key] = runners[cname](max(3, a.steps // 2), max(1, a.warmup))
     cpu = None if a.no_cpu else run_cpu_baseline(cfg, a.cpu_budget)
     line = {
         "metric": "reused KV tokens/sec (re-rotate+scatter) at Llama-3-8B shape; HBM GB/s",
