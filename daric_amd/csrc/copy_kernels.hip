@@ -260,9 +260,9 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_kernel(
 // e4m3 quantum). The kernel therefore rotates the code values directly and
 // saturates on requantisation; the registered scales are needed only where
 // cached values meet other data (kv_deviation).
-#ifndef DARIC_ROT_LANE_UNROLL
-#define DARIC_ROT_LANE_UNROLL 4
-#endif
+// Units in flight per lane in the lane kernel.
+constexpr int kRotLaneUnroll = 4;
+
 template <int KIND, bool NEOX>
 __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
     DescArg d, int job0, FastDiv njobs, RowGeomDiv gd, const float* __restrict__ inv_freq, int log2_parts) {
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void scatter_rotate_lane_kernel(
     // bf16 the register form measured 1% faster. Both give identical bits.
     constexpr bool CSL = KIND == kE4M3;
     constexpr int NC = CSL ? 1 : (NEOX ? VE : VE / 2);  // cos/sin values per lane
-    constexpr int UNR = DARIC_ROT_LANE_UNROLL;
+    constexpr int UNR = kRotLaneUnroll;
     __shared__ float s_cos[kMaxHalfRot];
     __shared__ float s_sin[kMaxHalfRot];
     __shared__ float4 s_cs[kMaxHalfRot / 2];   // CSL: (cos, sin) of pairs 2i and 2i+1
