@@ -325,6 +325,15 @@ def test_selection_fuzz(dev, data):
     if quant:
         km = (torch.randn(L, T, H, D, generator=g) * 4).to(new_dtype)
         vm = (torch.randn(L, T, H, D, generator=g) * 4).to(new_dtype)
+        if data.draw(st.booleans(), label="special values"):
+            # signed zeros, infinities, NaNs of both signs, subnormals and
+            # saturating magnitudes at random places of the rows
+            special = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), float("nan"), -float("nan"),
+                                    1e-6, -3e-7, 6e4, -6e4]).to(new_dtype)
+            for rows in (km, vm):
+                flat = rows.view(-1)
+                pos = torch.randint(0, flat.numel(), (max(1, flat.numel() // 50),), generator=g)
+                flat[pos] = special[torch.randint(0, len(special), (len(pos),), generator=g)]
         ks = (0.002 + 0.02 * torch.rand(L, H, generator=g)).float()
         vs = (0.002 + 0.02 * torch.rand(L, H, generator=g)).float()
     elif dtype == torch.uint8:
