@@ -18,7 +18,7 @@ import torch
 LIB_PATH = os.environ.get("DARIC_AMD_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "_lib", "libdaric_cache_ops.so")
 MAX_DIMS = 8
-ABI_VERSION = 4
+ABI_VERSION = 5
 ERR_VALUE = 5
 
 DTYPE_CODES = {
@@ -55,7 +55,7 @@ class DaricRopeSegment(ctypes.Structure):
 
 class DaricChunk(ctypes.Structure):
     _fields_ = [("bt_offset", c_int64), ("row_offset", c_int64), ("n_tokens", c_int64),
-                ("k", c_int64)]
+                ("k", c_int64), ("tok_start", c_int64)]
 
 
 P = POINTER

@@ -8,7 +8,9 @@ Here every re-rotation request becomes a list of same-shift segments
 (bt_offset, tok_start, n_tokens, delta) over one concatenated block table,
 and one rerotate_pages call covers every layer that shares a cache geometry
 and rotary embedding; cos/sin are formed from the rotary inverse frequencies
-in registers on the GPU.
+in registers on the GPU. Those frequencies are checked once per rotary module
+against its cos_sin_cache, the table the reference rotates with; a table
+they do not reproduce raises ValueError instead of rotating by another angle.
 
 Layer topology. The reference reads the process-global
 ProcessLocalConfig.cache_topo (configs/engine.py:11-70, 73-161) at
@@ -27,6 +29,7 @@ Bad cache layouts raise ValueError with the reference's text
 """
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass, field
 from typing import List, Optional, Sequence
 
@@ -34,7 +37,7 @@ import numpy as np
 import torch
 
 from . import cache_ops
-from .policy import DARICPolicy
+from .policy import DARICPolicy, plan_selection
 
 __all__ = ["AdaptionConfig", "LayerCacheTopo", "CacheTopo", "Adapter", "plan_load_segments",
            "plan_multi_segments", "check_rerotate_layout"]
@@ -125,16 +128,91 @@ def plan_multi_segments(group_ptrs, block_ids_list, group_idx: int):
     return np.asarray(bt, dtype=np.int32), segs
 
 
-def _inv_freq(rotary) -> torch.Tensor:
-    """fp32 inverse frequencies of a rotary embedding: an `inv_freq` attribute,
-    else vLLM's RotaryEmbedding._compute_inv_freq(base) (which the llama3 /
-    YaRN subclasses override with their scaled frequencies)."""
+def _table_positions(max_pos: int) -> list:
+    """Positions at which a rotary table is checked: 0..3, every power of two
+    and 1.5 times it below max_pos, and max_pos - 1. An inverse frequency that
+    differs from the table's by e (mod 2*pi) drifts by p*e at position p, so
+    the first power of two at which the drift passes the tolerance, or the last
+    position, shows it before it can wrap round."""
+    pos = {0, 1, 2, 3, max_pos - 1}
+    p = 4
+    while p < max_pos:
+        pos.update((p, p + p // 2))
+        p *= 2
+    return sorted(x for x in pos if 0 <= x < max_pos)
+
+
+def _inv_freq_candidates(rotary):
+    """Inverse-frequency vectors a vLLM rotary module can have built its table
+    from: an `inv_freq` attribute; _compute_inv_freq(base) (the default and
+    llama3-scaled embeddings); _compute_inv_freq(scaling_factor) (the YaRN
+    family's signature)."""
     inv = getattr(rotary, "inv_freq", None)
-    if inv is None and hasattr(rotary, "_compute_inv_freq"):
-        inv = rotary._compute_inv_freq(rotary.base)
-    if inv is None:
-        raise RuntimeError("rotary embedding exposes neither inv_freq nor _compute_inv_freq(base)")
-    return torch.as_tensor(inv).detach().to(torch.float32).reshape(-1)
+    if inv is not None:
+        yield "inv_freq", inv
+    fn = getattr(rotary, "_compute_inv_freq", None)
+    if fn is None:
+        return
+    for attr in ("base", "scaling_factor"):
+        arg = getattr(rotary, attr, None)
+        if arg is None:
+            continue
+        try:
+            yield f"_compute_inv_freq({attr})", fn(arg)
+        except Exception:       # a signature that does not take this argument
+            continue
+
+
+def _inv_freq(rotary) -> torch.Tensor:
+    """fp32 inverse frequencies that reproduce the rotary module's own table,
+    rotary.cos_sin_cache: the table the reference's rotation reads
+    (adapter.py:177-181, 271-283). The table is vLLM's layout,
+    [max_pos, rotary_dim] = m * cat(cos(p * inv_freq), sin(p * inv_freq)),
+    with m = cos_sin_cache[0, 0] its own scale (1, or YaRN's mscale). A
+    candidate (see _inv_freq_candidates) is taken when, at every position of
+    _table_positions, cos_sin_cache[p] / m is within
+    eps(table dtype) + 2^-22 * (1 + p * inv_freq[i]) of cos / sin of the float32
+    angle float32(p) * inv_freq[i] (the second term allows for the rounding of
+    the table's own angle). No candidate matching -- positions scaled by a
+    factor, a base other than rotary.base, a table of another form -- raises
+    ValueError naming the class, since rotating by another angle would
+    silently move K rows to the wrong position.
+
+    The scale m is not applied: the rotation by a shift d is the unit rotation
+    by d * inv_freq, as K computed at the new position would carry it. (The
+    reference's combined table carries m squared, adapter.py:280-281.)"""
+    name = type(rotary).__name__
+    R = int(rotary.rotary_dim)
+    table = getattr(rotary, "cos_sin_cache", None)
+    if not isinstance(table, torch.Tensor) or table.ndim < 2 or table.shape[0] < 1:
+        raise ValueError(f"{name}: rotary embedding has no [max_pos, rotary_dim] cos_sin_cache tensor")
+    table = table.detach().reshape(table.shape[0], -1)
+    if table.shape[1] != R or not table.is_floating_point():
+        raise ValueError(f"{name}: cos_sin_cache of shape {tuple(rotary.cos_sin_cache.shape)} and dtype "
+                         f"{table.dtype} is not a [max_pos, rotary_dim={R}] table of cos and sin")
+    pos = _table_positions(int(table.shape[0]))
+    rows = table.index_select(0, torch.tensor(pos, device=table.device)).to("cpu", torch.float64)
+    m = float(rows[0, 0])
+    if not (math.isfinite(m) and m > 0.0):
+        raise ValueError(f"{name}: cos_sin_cache[0, 0] = {m} is not a positive scale")
+    rows = rows / m
+    eps = torch.finfo(table.dtype).eps
+    p32 = torch.tensor(pos, dtype=torch.float32)[:, None]
+    tried = []
+    for label, cand in _inv_freq_candidates(rotary):
+        inv = torch.as_tensor(cand).detach().to("cpu", torch.float32).reshape(-1)
+        tried.append(label)
+        if inv.numel() != R // 2 or not bool(torch.isfinite(inv).all()):
+            continue
+        ang = (p32 * inv[None, :]).to(torch.float64)          # float32 product, as the kernels form it
+        tol = eps + 2.0 ** -22 * (1.0 + ang.abs())
+        want = torch.cat([ang.cos(), ang.sin()], dim=1)
+        if bool(((rows - want).abs() <= torch.cat([tol, tol], dim=1)).all()):
+            return inv.contiguous()
+    raise ValueError(
+        f"{name}: rotary cos_sin_cache is not cos/sin(p * inv_freq) for any inverse frequencies the "
+        f"module exposes (tried: {', '.join(tried) or 'none'}); re-rotation supports tables of that form "
+        f"only (default, llama3- and YaRN-scaled frequencies)")
 
 
 def check_rerotate_layout(layer_name: str, kv: torch.Tensor, page_first: bool, rotary_dim: int) -> None:
@@ -211,13 +289,23 @@ class Adapter:
         return len(self.rotary_embeds) == self.num_layers
 
     # ------------------------------------------------------------ rotation
-    def _device_inv_freq(self, rotary, device) -> torch.Tensor:
-        key = (id(rotary), str(device))
+    def _host_inv_freq(self, rotary) -> torch.Tensor:
+        """_inv_freq(rotary), checked against the module's table once per
+        (module, table storage)."""
+        table = getattr(rotary, "cos_sin_cache", None)
+        key = (id(rotary), table.data_ptr() if isinstance(table, torch.Tensor) else None)
         hit = self._inv_cache.get(key)
         if hit is None or hit[0] is not rotary:
-            hit = (rotary, _inv_freq(rotary).to(device).contiguous())
+            hit = (rotary, _inv_freq(rotary), {})
             self._inv_cache[key] = hit
-        return hit[1]
+        return hit
+
+    def _device_inv_freq(self, rotary, device) -> torch.Tensor:
+        hit = self._host_inv_freq(rotary)
+        dev = hit[2].get(str(device))
+        if dev is None:
+            dev = hit[2][str(device)] = hit[1].to(device).contiguous()
+        return dev
 
     def _rotate(self, layer_names: Sequence[str], plan) -> None:
         """Runs `plan(group_idx) -> (block table, segments)` for every KV-cache
@@ -242,6 +330,7 @@ class Adapter:
                 rotary = self.rotary_embeds[name]
                 page_first = bool(topo.layers[name].page_first)
                 check_rerotate_layout(name, kv, page_first, int(rotary.rotary_dim))
+                self._host_inv_freq(rotary)     # a table the kernels cannot reproduce raises here
                 key = (tuple(kv.shape), kv.stride(), kv.dtype, page_first, id(rotary),
                        int(rotary.rotary_dim), bool(rotary.is_neox_style))
                 batches.setdefault(key, (rotary, page_first, []))[2].append(kv)
@@ -272,3 +361,15 @@ class Adapter:
         if self.recompute_policy is None:
             return []
         return self.recompute_policy.get_recompute_ptrs(group_ptr)
+
+    def plan_recompute_selection(self, group_ptrs, block_ids_list, group_idx: int = 0,
+                                 no_recompute_lengths=None):
+        """(block table int32, chunks int64 [n, 5], rows) for a batch of
+        requests: each group of each request is one selection chunk whose k is
+        the number of tokens get_recompute_length's ranges put in it
+        (policy.plan_selection), over the requests' block lists of KV-cache
+        group `group_idx`. None without a recompute policy."""
+        if self.recompute_policy is None:
+            return None
+        return plan_selection(self.recompute_policy, group_ptrs,
+                              [b[group_idx] for b in block_ids_list], no_recompute_lengths)

@@ -302,11 +302,17 @@ def rerotate_pages(layers: Sequence[torch.Tensor], page_first: bool, block_table
 
 def _chunks(chunks):
     """(pointer to daric_chunk[n], n, keep-alive) from a sequence of
-    (bt_offset, row_offset, n_tokens, k) tuples or an int64 [n, 4] array."""
-    a = np.ascontiguousarray(np.asarray(chunks, dtype=np.int64).reshape(-1, 4))
-    if a.shape[0] == 0:
-        a = np.zeros((1, 4), np.int64)
+    (bt_offset, row_offset, n_tokens, k[, tok_start]) tuples or an int64
+    [n, 4] / [n, 5] array; tok_start defaults to 0."""
+    a = np.asarray(chunks, dtype=np.int64)
+    if a.size == 0:
+        a = np.zeros((1, 5), np.int64)
         return ctypes.cast(a.ctypes.data, ctypes.POINTER(DaricChunk)), 0, a
+    if a.ndim != 2 or a.shape[1] not in (4, 5):
+        raise ValueError("chunks must be (bt_offset, row_offset, n_tokens, k[, tok_start]) entries")
+    if a.shape[1] == 4:
+        a = np.concatenate([a, np.zeros((a.shape[0], 1), np.int64)], axis=1)
+    a = np.ascontiguousarray(a)
     return ctypes.cast(a.ctypes.data, ctypes.POINTER(DaricChunk)), a.shape[0], a
 
 
@@ -315,7 +321,8 @@ def kv_deviation(layers: Sequence[torch.Tensor], page_first: bool, block_table: 
                  stream: int = 0, k_scales: Optional[torch.Tensor] = None) -> torch.Tensor:
     """keys[l, row] = sum over (h, d) of (k_new - cached K)^2 in the fixed
     order of daric_amd/csrc/select_kernels.hip. chunks: (bt_offset,
-    row_offset, n_tokens, k). k_scales: [L, H] fp32 per-head scales of an fp8
+    row_offset, n_tokens, k[, tok_start]); token j of a chunk is token
+    tok_start + j of the block list at block_table[bt_offset]. k_scales: [L, H] fp32 per-head scales of an fp8
     cache (None: scale 1)."""
     layers = list(layers)
     dev = layers[0].device

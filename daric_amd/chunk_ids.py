@@ -29,7 +29,7 @@ import numpy as np
 import xxhash
 
 __all__ = ["token_ids_to_bytes", "get_hash_id", "split_chunk_ptr", "prefix_chunk_ids",
-           "independent_chunk_ids"]
+           "independent_chunk_ids", "ChunkLengthMismatch"]
 
 
 def token_ids_to_bytes(token_ids: Sequence[int]) -> bytes:
@@ -78,6 +78,13 @@ def _chain(tokens, bounds, restart, system_prefix: str) -> List[Tuple[str, List[
     return out
 
 
+class ChunkLengthMismatch(ValueError, AssertionError):
+    """The prompt's token count differs from the end of its group boundaries.
+    The reference's IndependentSearcher.search asserts this (searcher.py:145),
+    so callers written against it catch AssertionError; this error is both an
+    AssertionError and a ValueError."""
+
+
 def prefix_chunk_ids(tokens: Sequence[int], ind_ptr: Sequence[int], max_chunk_len: int,
                      system_prefix: str) -> List[Tuple[str, List[int]]]:
     """(id, [start, end)) of every piece, one chain through the whole prompt
@@ -91,7 +98,8 @@ def independent_chunk_ids(tokens: Sequence[int], ind_ptr: Sequence[int], max_chu
     """(id, [start, end)) of every piece, the chain restarting at every group
     (the reference's IndependentSearcher, searcher.py:133-149)."""
     if len(tokens) != ind_ptr[-1]:
-        raise ValueError(f"the prompt has {len(tokens)} tokens but its group boundaries end at {ind_ptr[-1]}")
+        raise ChunkLengthMismatch(
+            f"the prompt has {len(tokens)} tokens but its group boundaries end at {ind_ptr[-1]}")
     bounds, groups = split_chunk_ptr(ind_ptr, max_chunk_len)
     starts = np.asarray(bounds[:-1], dtype=np.int64)
     group_of = np.searchsorted(np.asarray(groups, dtype=np.int64), starts, side="right") - 1

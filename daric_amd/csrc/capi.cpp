@@ -1109,15 +1109,20 @@ Chunks build_chunks(const daric_chunk* chunks, int64_t n, int64_t PS, int64_t bt
     c.v.reserve(n);
     for (int64_t i = 0; i < n; ++i) {
         const daric_chunk& s = chunks[i];
-        DARIC_CHECK(s.n_tokens >= 0 && s.row_offset >= 0 && s.bt_offset >= 0 && s.k >= 0,
-                    "negative chunk field at chunk ", i);
+        DARIC_CHECK(s.n_tokens >= 0 && s.row_offset >= 0 && s.bt_offset >= 0 && s.k >= 0 &&
+                    s.tok_start >= 0, "negative chunk field at chunk ", i);
         DARIC_CHECK(s.n_tokens <= kIntMax && s.k <= kIntMax, "chunk too long at chunk ", i);
+        DARIC_CHECK(s.tok_start <= kIntMax && s.bt_offset <= kInt64Max - kIntMax, "chunk ", i,
+                    " starts too far into its block list");
         DARIC_CHECK(s.row_offset + s.n_tokens <= T, "chunk ", i, " rows exceed the recomputed tensor");
+        // the chunk's first page, and its first token's place in that page
+        const int64_t bt_first = s.bt_offset + s.tok_start / PS;
         if (s.n_tokens > 0)
-            DARIC_CHECK(s.bt_offset + (s.n_tokens - 1) / PS < bt_n, "chunk ", i,
+            DARIC_CHECK(bt_first + (s.tok_start % PS + s.n_tokens - 1) / PS < bt_n, "chunk ", i,
                         " reads past the end of block_table");
         SelChunk sc{};
-        sc.bt_offset = s.bt_offset;
+        sc.bt_offset = bt_first;
+        sc.tok0 = static_cast<int32_t>(s.tok_start % PS);
         sc.row_offset = s.row_offset;
         sc.n_tokens = static_cast<int32_t>(s.n_tokens);
         sc.k = static_cast<int32_t>(s.k);
@@ -1269,7 +1274,7 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
             if (g.v_off >= 0) check_scales(v_scales, "v_scales");
             DARIC_CHECK(merge_fits_rows(g, t.elem_size, true),
                         "quantising merge_rows needs head_dim % 8 == 0, 8-byte aligned cache rows and K+V "
-                        "rows of at most 64 KiB of recomputed values");
+                        "rows of at most ", merge_max_row_bytes() / 1024, " KiB of recomputed values per token");
             for (int64_t i = 0; i < n_layers; ++i)
                 DARIC_CHECK(aligned(layers[i].data, 8), "misaligned layer ", i);
         } else {
@@ -1284,7 +1289,10 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
                     "sel_idx must be a contiguous int32 [n_layers, n_chunks, kmax] tensor");
         const int64_t kmax = sel_idx->sizes[2];
         Chunks c = build_chunks(chunks, n_chunks, g.PS, numel(*block_table), T, 1);
-        if (kmax == 0) return;
+        // Nothing is selected (no rows, no chunk with k > 0 and tokens, or no
+        // index slots): no launch, so empty k_new / v_new (whose data pointer
+        // may be null) are never read.
+        if (kmax == 0 || T == 0 || c.max_k == 0) return;
         DeviceGuard guard(t.device);
         const hipStream_t st = as_stream(stream);
         const size_t cb = c.v.size() * sizeof(SelChunk);

@@ -128,7 +128,7 @@ struct SelChunk {
     int32_t n_tokens;
     int32_t k;
     int32_t tile_begin;
-    int32_t pad0;
+    int32_t tok0;          // position of token 0 in the page at bt_offset (0 <= tok0 < PS)
 };
 
 }  // namespace daric

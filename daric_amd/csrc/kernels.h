@@ -131,8 +131,10 @@ void launch_topk(const float* keys, int n_layers, int64_t T, const DescArg& d,
 // merge: quant_from is -1 (rows are copied as bytes) or the ElemKind of
 // bf16 / fp16 rows quantised into an e4m3 cache with the [n_layers, H] fp32
 // k_scales / v_scales. merge_fits_rows: whether the row kernel takes the
-// geometry (required for quantising).
+// geometry (required for quantising); merge_max_row_bytes: the most bytes of
+// recomputed K+V values per token it takes.
 bool merge_fits_rows(const KVGeom& g, int elem_size, bool quant);
+int64_t merge_max_row_bytes();
 void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int elem_size,
                   const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,
                   int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, int quant_from,

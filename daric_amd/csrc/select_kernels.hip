@@ -114,9 +114,10 @@ __global__ __launch_bounds__(kThreads) void deviation_kernel(
     for (int i = 0; i < kTokPerWave; ++i) {
         const int j = j0 + i;
         int blk = -1;
-        if (j < c.n_tokens) blk = bt[c.bt_offset + j / g.PS];
+        const int p = c.tok0 + j;                  // position in the chunk's block list
+        if (j < c.n_tokens) blk = bt[c.bt_offset + p / g.PS];
         valid[i] = j < c.n_tokens && blk >= 0 && blk < g.num_blocks;
-        cache_row[i] = static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(j % g.PS) * g.ss;
+        cache_row[i] = static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(p % g.PS) * g.ss;
         new_row[i] = k_new + ((static_cast<int64_t>(l) * T + c.row_offset + j) * N) * 2;
     }
 
@@ -320,9 +321,10 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(
         const int j = srow[q];
         if (j < 0 || j >= c.n_tokens) continue;
         if (kv == 1 && g.v_off < 0) continue;
-        const int blk = bt[c.bt_offset + j / g.PS];
+        const int p = c.tok0 + j;
+        const int blk = bt[c.bt_offset + p / g.PS];
         if (blk <= 0 || blk >= g.num_blocks) continue;
-        const int64_t dst_el = static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(j % g.PS) * g.ss +
+        const int64_t dst_el = static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(p % g.PS) * g.ss +
                                static_cast<int64_t>(h) * g.sh + (kv ? g.v_off : 0);
         const uint8_t* src = (kv ? v_new : k_new) +
                              (static_cast<int64_t>(l) * T + c.row_offset + j) * rowbytes +
@@ -381,10 +383,11 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
         if (q < min(kmax, c.k)) {
             const int j = sel[(static_cast<int64_t>(l) * n_chunks + ci) * kmax + q];
             if (j >= 0 && j < c.n_tokens) {
-                const int blk = bt[c.bt_offset + j / g.PS];
+                const int p = c.tok0 + j;
+                const int blk = bt[c.bt_offset + p / g.PS];
                 if (blk > 0 && blk < g.num_blocks) {
                     src = (static_cast<int64_t>(l) * T + c.row_offset + j) * row_bytes;
-                    dst = (static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(j % g.PS) * g.ss) * ces;
+                    dst = (static_cast<int64_t>(blk) * g.sb + static_cast<int64_t>(p % g.PS) * g.ss) * ces;
                 }
             }
         }
@@ -501,6 +504,8 @@ bool merge_fits_rows(const KVGeom& g, int elem_size, bool quant) {
     const int64_t tok_units = static_cast<int64_t>(g.v_off >= 0 ? 2 : 1) * g.H * (g.D * ses / 16);
     return tok_units <= static_cast<int64_t>(kMergeThreads) * kMergeUnits;
 }
+
+int64_t merge_max_row_bytes() { return static_cast<int64_t>(kMergeThreads) * kMergeUnits * 16; }
 
 void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int elem_size,
                   const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,

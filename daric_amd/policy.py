@@ -24,16 +24,20 @@ recomputed tokens:
 The outputs hinge on the float32 solve and the half-to-even rounding, so they
 are pinned by vectors of the reference's own function
 (tests/golden/policy_vectors.json). The selection kernels take the per-chunk
-counts this policy implies (see recompute_counts).
+counts this policy implies: recompute_counts turns ranges into per-group
+counts, selection_chunks / plan_selection turn a request's (or a batch's)
+group boundaries and block lists into the chunks kv_deviation,
+topk_per_chunk and merge_rows take.
 """
 from __future__ import annotations
 
 import math
 from typing import Callable
 
+import numpy as np
 import torch
 
-__all__ = ["DARICPolicy", "cluster_groups", "recompute_counts"]
+__all__ = ["DARICPolicy", "cluster_groups", "recompute_counts", "selection_chunks", "plan_selection"]
 
 
 def cluster_groups(ranges):
@@ -119,12 +123,70 @@ class DARICPolicy:
         return ranges
 
 
+def _union(ranges):
+    """Disjoint sorted [start, end) ranges covering the same tokens."""
+    out = []
+    for s, e in sorted((int(s), int(e)) for s, e in ranges if e > s):
+        if out and s <= out[-1][1]:
+            out[-1][1] = max(out[-1][1], e)
+        else:
+            out.append([s, e])
+    return out
+
+
 def recompute_counts(group_ptr, ranges):
     """Tokens of each group [g_i, g_{i+1}) covered by `ranges`: the per-chunk
     k a deviation-based selection (topk_per_chunk) can spend in place of the
-    positional choice."""
+    positional choice. A token is counted once even where ranges overlap (the
+    policy's last widening can reach back over ranges it no longer merges,
+    and the reference then recomputes those tokens twice)."""
+    union = _union(ranges)
     counts = []
     for i in range(len(group_ptr) - 1):
         lo, hi = group_ptr[i], group_ptr[i + 1]
-        counts.append(sum(max(0, min(e, hi) - max(s, lo)) for s, e in ranges))
+        counts.append(sum(max(0, min(e, hi) - max(s, lo)) for s, e in union))
     return counts
+
+
+def selection_chunks(group_ptr, ranges, bt_offset: int = 0, row_offset: int = 0,
+                     no_recompute_length=None):
+    """The selection kernels' chunks for one request: one
+    (bt_offset, row_offset, n_tokens, k, tok_start) entry per group i, spanning
+    tokens [g_i, g_{i+1}), with k the tokens of `ranges` (the policy's
+    get_recompute_ptrs output) inside the group (recompute_counts). Group i
+    starts at token g_i - g_0 of the request's block list, which begins at
+    block_table[bt_offset] (as apply_rerotate_multi places groups,
+    adapter.py:162-171), and at row row_offset + g_i - g_0 of the recomputed
+    K/V tensors. no_recompute_length: ranges ending at or before it are dropped
+    first, as the worker drops ranges inside the prefix the GPU still holds
+    (worker.py:322-324). So topk_per_chunk picks, per group, as many tokens as
+    the policy would recompute there, by K deviation instead of position."""
+    if no_recompute_length is not None:
+        ranges = [[s, e] for s, e in ranges if e > no_recompute_length]
+    counts = recompute_counts(group_ptr, ranges) if ranges else [0] * (len(group_ptr) - 1)
+    g0 = group_ptr[0]
+    return [(int(bt_offset), int(row_offset + lo - g0), int(hi - lo), int(k), int(lo - g0))
+            for (lo, hi), k in zip(zip(group_ptr[:-1], group_ptr[1:]), counts)]
+
+
+def plan_selection(policy: DARICPolicy, group_ptrs, block_ids_list, no_recompute_lengths=None):
+    """Chunks of a batch of requests for kv_deviation / topk_per_chunk /
+    merge_rows. Request r contributes its block list (block_ids_list[r],
+    concatenated into one int32 block table in request order) and its tokens
+    g_0..g_n - 1 (consecutive rows of the recomputed tensors, requests in
+    order); each of its groups is one chunk whose k the policy sets (0 for
+    a request of one group, which the policy leaves alone). Returns
+    (block_table int32 [sum of block list lengths], chunks int64 [n, 5],
+    number of recomputed rows)."""
+    bt: list = []
+    chunks: list = []
+    rows = 0
+    for r, (group_ptr, blocks) in enumerate(zip(group_ptrs, block_ids_list)):
+        if isinstance(blocks, torch.Tensor):
+            blocks = blocks.tolist()
+        ranges = policy.get_recompute_ptrs(list(group_ptr))
+        nr = None if no_recompute_lengths is None else no_recompute_lengths[r]
+        chunks += selection_chunks(group_ptr, ranges, len(bt), rows, nr)
+        bt.extend(int(b) for b in blocks)
+        rows += int(group_ptr[-1] - group_ptr[0])
+    return (np.asarray(bt, dtype=np.int32), np.asarray(chunks, dtype=np.int64).reshape(-1, 5), rows)

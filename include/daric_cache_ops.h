@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DARIC_ABI_VERSION 4
+#define DARIC_ABI_VERSION 5
 
 /* Status codes. */
 #define DARIC_OK 0
@@ -279,14 +279,20 @@ int daric_rerotate_pages(const daric_tensor* layers, int64_t n_layers, int page_
 /* ---------------------------------------------------------------------- */
 
 /* A chunk of consecutive tokens of one request: token j (0 <= j < n_tokens)
- * lives at slot block_table[bt_offset + j / PS] * PS + j % PS of the paged
- * cache and at row row_offset + j of the contiguous recomputed tensors.
- * `k` is the number of tokens to select in it. */
+ * is token p = tok_start + j of the block list that begins at
+ * block_table[bt_offset], so it lives at slot
+ * block_table[bt_offset + p / PS] * PS + p % PS of the paged cache, and at
+ * row row_offset + j of the contiguous recomputed tensors. `k` is the number
+ * of tokens to select in it. tok_start lets a chunk begin inside a page, as
+ * the groups of a request do (group i of the reference's group_ptr starts at
+ * token group_ptr[i] - group_ptr[0] of the request's blocks,
+ * daric/adaption/adapter.py:127-171). */
 typedef struct daric_chunk {
     int64_t bt_offset;
     int64_t row_offset;
     int64_t n_tokens;
     int64_t k;
+    int64_t tok_start;
 } daric_chunk;
 
 /* keys[l, row_offset + j] = sum over (h, d) of (k_new[l, row, h, d] - K_cache)^2

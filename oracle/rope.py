@@ -111,6 +111,64 @@ def rotate_slots(layer: torch.Tensor, page_first: bool, slots, delta: int,
     kv[blk, s] = _from_values(out, layer.dtype, scale)
 
 
+def table_cos_sin_load(cos_sin_cache, old_pos, new_pos):
+    """Per-token combined cos/sin [n, R/2] of apply_rerotate_load as the
+    reference forms them from the rotary table (adapter.py:271-283):
+    cos = cos(new)cos(old) + sin(new)sin(old), sin = sin(new)cos(old) -
+    cos(new)sin(old), here in float64 from the table's values. The table is
+    first divided by its own scale m = cos_sin_cache[0, 0]: the reference's
+    combined values carry m squared, the re-rotation here is the unit rotation
+    (rows keep their norm)."""
+    t = _unit_table(cos_sin_cache)
+    half = t.shape[1] // 2
+    o, n = t[np.asarray(old_pos, dtype=np.int64)], t[np.asarray(new_pos, dtype=np.int64)]
+    oc, os_, nc, ns = o[:, :half], o[:, half:], n[:, :half], n[:, half:]
+    return nc * oc + ns * os_, ns * oc - nc * os_
+
+
+def table_cos_sin_multi(cos_sin_cache, deltas):
+    """Per-token cos/sin [n, R/2] of apply_rerotate_multi: the table row of
+    the shift itself (adapter.py:147-150, 176-181), divided by m as above."""
+    t = _unit_table(cos_sin_cache)
+    half = t.shape[1] // 2
+    r = t[np.asarray(deltas, dtype=np.int64)]
+    return r[:, :half], r[:, half:]
+
+
+def _unit_table(cos_sin_cache) -> np.ndarray:
+    t = torch.as_tensor(cos_sin_cache).detach().to("cpu", torch.float64)
+    t = t.reshape(t.shape[0], -1).numpy()
+    return t / t[0, 0]
+
+
+def rotate_slots_cs(layer: torch.Tensor, page_first: bool, slots, cos, sin, rotary_dim: int,
+                    is_neox: bool) -> None:
+    """Rotate in place the K rows (all heads) of slot i by its own (cos[i],
+    sin[i]) rows, with the pairing and formula of _fused_rerotate_kernel
+    (adapter.py:57-88), in float64 (16-bit caches). Slots must be distinct."""
+    kv = k_view(layer, page_first, rotary_dim)
+    ps = kv.shape[1]
+    slots = np.asarray(list(slots), dtype=np.int64)
+    if slots.size == 0:
+        return
+    assert np.unique(slots).size == slots.size
+    R = int(rotary_dim)
+    blk, s = torch.from_numpy(slots // ps), torch.from_numpy(slots % ps)
+    x = kv[blk, s].to(torch.float64).numpy()         # [n, H, D]
+    c = np.asarray(cos, dtype=np.float64)[:, None, :]
+    sn = np.asarray(sin, dtype=np.float64)[:, None, :]
+    out = x.copy()
+    if is_neox:
+        x1, x2 = x[..., : R // 2], x[..., R // 2: R]
+        out[..., : R // 2] = x1 * c - x2 * sn
+        out[..., R // 2: R] = x2 * c + x1 * sn
+    else:
+        x1, x2 = x[..., 0:R:2], x[..., 1:R:2]
+        out[..., 0:R:2] = x1 * c - x2 * sn
+        out[..., 1:R:2] = x2 * c + x1 * sn
+    kv[blk, s] = torch.from_numpy(out.astype(np.float32)).to(layer.dtype)
+
+
 def segment_slots(block_table, bt_offset: int, tok_start: int, n_tokens: int,
                   page_size: int) -> list[int]:
     """Slots of a run of tokens (adapter.py:164-170, 258-264)."""

@@ -91,14 +91,22 @@ def fixed_order_sumsq(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     return key
 
 
-def chunk_slots(block_table, bt_offset, n_tokens, page_size):
+def _fields(chunk):
+    """(bt_offset, row_offset, n_tokens, k, tok_start) of a 4- or 5-field chunk."""
+    c = [int(x) for x in chunk]
+    return tuple(c) if len(c) == 5 else tuple(c) + (0,)
+
+
+def chunk_slots(block_table, bt_offset, n_tokens, page_size, tok_start=0):
+    """(block id, place in page) of chunk-local tokens 0..n_tokens-1: token j is
+    token tok_start + j of the block list at block_table[bt_offset]."""
     bt = np.asarray(block_table)
-    j = np.arange(n_tokens)
-    return bt[bt_offset + j // page_size].astype(np.int64), j % page_size
+    p = tok_start + np.arange(n_tokens)
+    return bt[bt_offset + p // page_size].astype(np.int64), p % page_size
 
 
 def deviation(layers, page_first, block_table, k_new, chunks, k_scales=None) -> np.ndarray:
-    """keys [L, T] for chunks (bt_offset, row_offset, n_tokens, k); rows of T
+    """keys [L, T] for chunks (bt_offset, row_offset, n_tokens, k[, tok_start]); rows of T
     not covered by any chunk are left 0, and so are tokens whose block id lies
     outside [0, num_blocks)."""
     L, T = len(layers), k_new.shape[1]
@@ -108,8 +116,9 @@ def deviation(layers, page_first, block_table, k_new, chunks, k_scales=None) -> 
         ps, h, d = kv.shape[1], kv.shape[2], kv.shape[3]
         ks = None if k_scales is None else k_scales[l]
         nb = kv.shape[0]
-        for bt_offset, row_offset, n_tokens, _k in chunks:
-            blk, s = chunk_slots(block_table, bt_offset, n_tokens, ps)
+        for chunk in chunks:
+            bt_offset, row_offset, n_tokens, _k, tok_start = _fields(chunk)
+            blk, s = chunk_slots(block_table, bt_offset, n_tokens, ps, tok_start)
             ok = (blk >= 0) & (blk < nb)        # other block ids: not read, key 0
             cached = _as_f32(kv[torch.as_tensor(np.where(ok, blk, 0)), torch.as_tensor(s)], ks)
             cached = cached.reshape(n_tokens, h * d)
@@ -131,7 +140,8 @@ def topk_per_chunk(keys: np.ndarray, chunks, kmax: int) -> np.ndarray:
     L = keys.shape[0]
     out = np.full((L, len(chunks), kmax), -1, np.int32)
     for l in range(L):
-        for c, (_bt, row_offset, n_tokens, k) in enumerate(chunks):
+        for c, chunk in enumerate(chunks):
+            _bt, row_offset, n_tokens, k, _ts = _fields(chunk)
             sel = topk_chunk(keys[l, row_offset: row_offset + n_tokens], int(k))
             out[l, c, : len(sel)] = sel
     return out
@@ -164,14 +174,16 @@ def merge_rows(layers, page_first, block_table, k_new, v_new, chunks, sel_idx,
         vv = v_view(layer, page_first)
         nb, ps = kv.shape[0], kv.shape[1]
         rows, blks, slots = [], [], []
-        for c, (bt_offset, row_offset, n_tokens, _k) in enumerate(chunks):
+        for c, chunk in enumerate(chunks):
+            bt_offset, row_offset, n_tokens, _k, tok_start = _fields(chunk)
             j = sel_idx[l, c].astype(np.int64)
             j = j[(j >= 0) & (j < n_tokens)]
-            blk = bt[bt_offset + j // ps].astype(np.int64)
+            p = tok_start + j
+            blk = bt[bt_offset + p // ps].astype(np.int64)
             keep = (blk > 0) & (blk < nb)
             rows.append(row_offset + j[keep])
             blks.append(blk[keep])
-            slots.append(j[keep] % ps)
+            slots.append(p[keep] % ps)
         if not rows:
             continue
         r = torch.from_numpy(np.concatenate(rows))

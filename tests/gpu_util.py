@@ -102,18 +102,21 @@ def ulp(v: np.ndarray, dtype) -> np.ndarray:
 
 
 def assert_rotation_parity(got: torch.Tensor, want: torch.Tensor, mask: torch.Tensor,
-                           pnorm: torch.Tensor, max_ulps=1):
+                           pnorm: torch.Tensor, max_ulps=1, angle_tol=0.0):
     """Bit-exact outside `mask`. Inside: within max_ulps of the target dtype of
     the oracle value, plus an fp32 arithmetic allowance of 2^-20 times the
     pair's norm (the float32 rounding of x1*c - x2*s when it cancels; 2^12
-    below the bf16 resolution of the pair)."""
+    below the bf16 resolution of the pair), plus angle_tol (radians) times the
+    pair's norm where the oracle's angles come from another rounding of the
+    same angle (a rotary table's float32 entries)."""
     got = got.cpu()
     want = want.cpu()
     gi, wi = got.view(INT_VIEW[got.dtype]), want.view(INT_VIEW[want.dtype])
     bad = (gi != wi) & ~mask
     assert not bool(bad.any()), f"{int(bad.sum())} elements differ outside the rotated region"
     gv, wv = values(got[mask]), values(want[mask])
-    tol = max_ulps * ulp(np.maximum(np.abs(gv), np.abs(wv)), got.dtype) + 2.0 ** -20 * pnorm[mask].numpy()
+    tol = max_ulps * ulp(np.maximum(np.abs(gv), np.abs(wv)), got.dtype) + \
+        (2.0 ** -20 + angle_tol) * pnorm[mask].numpy()
     err = np.abs(gv - wv)
     worst = float((err / tol).max()) if err.size else 0.0
     if not (err <= tol).all():

@@ -1,6 +1,8 @@
 """Adapter counterpart, host side: segment planning against the oracle's
 restatement of apply_rerotate_load/multi (reference adapter.py:118-295),
 layer batching by group and geometry, the rerotate/recompute switches."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -8,6 +10,7 @@ import torch
 from daric_amd import adapter as ad
 from daric_amd.policy import DARICPolicy
 from oracle import rope as orope
+from tests import adapter_fakes as afakes
 from tests.adapter_fakes import FakeMeta, FakeRotary
 
 
@@ -104,5 +107,66 @@ def test_inv_freq_source():
 
     class Bare:
         rotary_dim, is_neox_style = 8, True
-    with pytest.raises(RuntimeError, match="inv_freq"):
+    with pytest.raises(ValueError, match="Bare: rotary embedding has no .* cos_sin_cache"):
         ad._inv_freq(Bare())
+
+
+@pytest.mark.parametrize("max_pos,dtype", [(64, torch.float32), (131072, torch.float32),
+                                           (131072, torch.bfloat16), (8192, torch.float16)])
+def test_inv_freq_accepts_the_default_table(max_pos, dtype):
+    r = FakeRotary(128, max_pos=max_pos, dtype=dtype)
+    np.testing.assert_array_equal(ad._inv_freq(r).numpy(), r._compute_inv_freq(r.base).numpy())
+
+
+@pytest.mark.parametrize("max_pos", [64, 8192, 131072])
+def test_inv_freq_refuses_tables_of_scaled_positions_or_another_base(max_pos):
+    """Tables the kernels' angle float32(d) * inv_freq cannot reproduce: the
+    re-rotation raises ValueError naming the class instead of rotating by
+    another angle."""
+    with pytest.raises(ValueError, match="ScaledPositionsRotary: rotary cos_sin_cache is not"):
+        ad._inv_freq(afakes.ScaledPositionsRotary(128, max_pos=max_pos))
+    with pytest.raises(ValueError, match="OtherBaseRotary: rotary cos_sin_cache is not"):
+        ad._inv_freq(afakes.OtherBaseRotary(128, max_pos=max_pos, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_inv_freq_accepts_a_scaled_table_of_yarn_form(dtype):
+    """m = cos_sin_cache[0, 0] = 1.25 is the table's own scale; the frequencies
+    come from _compute_inv_freq(scaling_factor) (YaRN's signature) after
+    _compute_inv_freq(base) fails the check."""
+    r = afakes.MScaleRotary(64, max_pos=16384, dtype=dtype)
+    np.testing.assert_array_equal(ad._inv_freq(r).numpy(), r._compute_inv_freq(r.scaling_factor).numpy())
+
+
+def test_inv_freq_check_catches_small_frequency_errors():
+    """A candidate off by one part in 10^5 drifts past the tolerance by the
+    table's last positions and is passed over; one off by a whole turn (2*pi)
+    is the same rotation at every integer position and is accepted."""
+    r = FakeRotary(64, max_pos=131072)
+    good = r._compute_inv_freq(r.base)
+    r.inv_freq = good * (1 + 1e-5)
+    np.testing.assert_array_equal(ad._inv_freq(r).numpy(), good.numpy())   # _compute_inv_freq(base)
+    r.base = 400000.0                                                      # now no candidate fits
+    with pytest.raises(ValueError, match=r"tried: inv_freq, _compute_inv_freq\(base\)"):
+        ad._inv_freq(r)
+    r3 = FakeRotary(64, max_pos=4096)
+    r3.inv_freq = good + 2 * math.pi
+    assert torch.equal(ad._inv_freq(r3), (good + 2 * math.pi).float())
+
+
+def test_table_positions_cover_every_power_of_two():
+    pos = ad._table_positions(131072)
+    assert pos[:4] == [0, 1, 2, 3] and pos[-1] == 131071
+    assert all((1 << k) in pos for k in range(17))
+    assert ad._table_positions(1) == [0]
+
+
+def test_rotation_refused_before_any_layer_moves(monkeypatch):
+    rec = Recorder()
+    monkeypatch.setattr(ad.cache_ops, "rerotate_pages", rec)
+    a, names = make_adapter()
+    a.rotary_embeds[names[3]] = afakes.OtherBaseRotary(32)
+    metas = [FakeMeta("a", [0, 20], 100, ([3, 4], [7, 8]))]
+    with pytest.raises(ValueError, match="OtherBaseRotary"):
+        a.apply_rerotate_load(metas)
+    assert rec.calls == []

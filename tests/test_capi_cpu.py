@@ -61,7 +61,7 @@ def test_exports_every_declared_symbol(lib):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover the header"
-    assert lib.daric_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.daric_abi_version() == _lib.ABI_VERSION == 5
 
 
 def fake(shape, dtype, device=0, strides=None, ptr=0x10000000):
@@ -419,3 +419,47 @@ def test_c_consumer_compiles_and_links(lib, tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "store buffer not registered" in out.stdout
+
+
+def test_merge_of_nothing_makes_no_device_call(lib):
+    """merge_rows with empty recomputed rows (null data pointer) or chunks
+    without tokens returns before any HIP call: with no GPU here, any launch
+    or device call would fail the call."""
+    layer = (_lib.DaricTensor * 1)(fake((2, 8, 16, 4, 64), torch.bfloat16))
+    bt = fake((8,), torch.int32, ptr=0x20000000)
+    empty = fake((1, 0, 4, 64), torch.bfloat16, ptr=0)
+    chunks = (_lib.DaricChunk * 2)(_lib.DaricChunk(0, 0, 0, 4, 0), _lib.DaricChunk(1, 0, 0, 5, 3))
+    sel = fake((1, 2, 5), torch.int32, ptr=0x50000000)
+    st = lib.daric_merge_rows(layer, 1, 0, ctypes.byref(bt), ctypes.byref(empty), ctypes.byref(empty),
+                              chunks, 2, ctypes.byref(sel), None, None, ctypes.c_uint64(0))
+    assert st == 0, lib.daric_last_error().decode()
+    # rows present but no chunk has tokens: still nothing to merge
+    rows = fake((1, 6, 4, 64), torch.bfloat16, ptr=0x60000000)
+    st = lib.daric_merge_rows(layer, 1, 0, ctypes.byref(bt), ctypes.byref(rows), ctypes.byref(rows),
+                              chunks, 2, ctypes.byref(sel), None, None, ctypes.c_uint64(0))
+    assert st == 0, lib.daric_last_error().decode()
+    # a chunk with tokens does reach the device (and fails here, without a GPU)
+    chunks[1].n_tokens = 6
+    st = lib.daric_merge_rows(layer, 1, 0, ctypes.byref(bt), ctypes.byref(rows), ctypes.byref(rows),
+                              chunks, 2, ctypes.byref(sel), None, None, ctypes.c_uint64(0))
+    assert st != 0
+
+
+def test_chunk_start_inside_a_page_is_checked_against_the_block_table(lib):
+    """tok_start moves a chunk's tokens along its block list: a chunk whose
+    last token falls past the block table is refused."""
+    layer = (_lib.DaricTensor * 1)(fake((2, 8, 16, 4, 64), torch.bfloat16))
+    bt = fake((4,), torch.int32, ptr=0x20000000)
+    rows = fake((1, 64, 4, 64), torch.bfloat16, ptr=0x60000000)
+    keys = fake((1, 64), torch.float32, ptr=0x70000000)
+
+    def run(bo, n, ts):
+        ch = (_lib.DaricChunk * 1)(_lib.DaricChunk(bo, 0, n, 1, ts))
+        st = lib.daric_kv_deviation(layer, 1, 0, ctypes.byref(bt), ctypes.byref(rows), ch, 1, None,
+                                    ctypes.byref(keys), ctypes.c_uint64(0))
+        return lib.daric_last_error().decode() if st else None
+
+    assert "reads past the end of block_table" in run(0, 49, 16)       # tokens 16..64: page 4
+    assert "reads past the end of block_table" in run(1, 40, 9)        # pages 1.. + (9 + 39) // 16 = 4
+    assert "negative chunk field" in run(0, 4, -1)
+    assert "reads past the end" not in (run(0, 48, 16) or "")           # tokens 16..63: pages 1-3

@@ -50,6 +50,9 @@ def test_independent_chain_is_position_free():
     assert ids_a == ids_b[: len(ids_a)] and len(ids_a) == 4
     with pytest.raises(ValueError):
         ci.independent_chunk_ids([1, 2, 3], [0, 4], 4, "m")
+    # the reference asserts the lengths (searcher.py:145): its callers catch AssertionError
+    with pytest.raises(AssertionError, match="3 tokens but its group boundaries end at 4"):
+        ci.independent_chunk_ids([1, 2, 3], [0, 4], 4, "m")
     with pytest.raises(OverflowError):
         ci.token_ids_to_bytes([-1])
 

@@ -151,3 +151,53 @@ def test_segment_planning():
     # relative position 10 with PS 16 is block bt[0] = 1, offset 10 -> slot 26
     assert rope.segment_slots(bt, 0, 10, 10, 16)[:2] == [26, 27]
     assert rope.segment_slots(bt, 0, 20, 15, 16)[-1] == 2 * 16 + 34 - 16
+
+
+def _complex_table(max_pos, inv_freq, m=1.0):
+    """m * cat(cos(p * theta), sin(p * theta)) from complex exponentials in float64."""
+    z = np.exp(1j * np.arange(max_pos)[:, None] * np.asarray(inv_freq, np.float64)[None, :])
+    return torch.from_numpy(np.concatenate([z.real, z.imag], axis=1) * m)
+
+
+@pytest.mark.parametrize("m", [1.0, 1.25])
+def test_table_cos_sin_is_the_angle_difference(m):
+    """The reference's combined rows (adapter.py:276-283) equal cos/sin of
+    (new - old) * theta by the angle-subtraction identity; multi's rows are
+    the shift's own row; the table scale m is divided out."""
+    inv = rope.default_inv_freq(64, 10000.0)
+    tab = _complex_table(3000, inv, m)
+    rng = np.random.default_rng(4)
+    old = rng.integers(0, 3000, 50)
+    new = rng.integers(0, 3000, 50)
+    c, s = rope.table_cos_sin_load(tab, old, new)
+    th = (new - old)[:, None] * inv.astype(np.float64)[None, :]
+    np.testing.assert_allclose(c, np.cos(th), atol=1e-12)
+    np.testing.assert_allclose(s, np.sin(th), atol=1e-12)
+    c2, s2 = rope.table_cos_sin_multi(tab, new)
+    th2 = new[:, None] * inv.astype(np.float64)[None, :]
+    np.testing.assert_allclose(c2, np.cos(th2), atol=1e-12)
+    np.testing.assert_allclose(s2, np.sin(th2), atol=1e-12)
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_rotate_slots_cs_is_complex_multiplication(neox):
+    """Per-slot rotation by its own angle row equals the textbook complex
+    form, slot by slot; V and dims >= R stay as they were."""
+    R, D, H = 32, 48, 2
+    inv = rope.default_inv_freq(R, 500000.0)
+    g = torch.Generator().manual_seed(2)
+    layer = torch.randn(2, 6, 16, H, D, generator=g, dtype=torch.float64).to(torch.float32)
+    before = layer.clone()
+    slots = [3, 17, 40, 95]
+    delta = np.array([5, -9, 700, 1])
+    th = delta[:, None] * inv.astype(np.float64)[None, :]
+    rope.rotate_slots_cs(layer, False, slots, np.cos(th), np.sin(th), R, neox)
+    for i, slot in enumerate(slots):
+        b, j = slot // 16, slot % 16
+        x = before[0, b, j].numpy().astype(np.float64)
+        want = rope_forward_complex(x, float(delta[i]), inv, R, neox)
+        np.testing.assert_allclose(layer[0, b, j].numpy(), want, rtol=1e-6, atol=1e-6)
+    assert torch.equal(layer[1], before[1])
+    mask = torch.ones(6 * 16, dtype=torch.bool)
+    mask[slots] = False
+    assert torch.equal(layer[0].reshape(96, H, D)[mask], before[0].reshape(96, H, D)[mask])
