@@ -69,6 +69,7 @@ SIGNATURES = {
     "daric_last_error": (c_char_p, []),
     "daric_timing_enable": (c_int, [c_int]),
     "daric_timing_read": (c_int, [P(c_double), I64P]),
+    "daric_debug_counters": (c_int, [I64P, I64P, I64P]),
     "daric_copier_create": (c_int, [P(c_void_p)]),
     "daric_copier_destroy": (c_int, [c_void_p]),
     "daric_copier_register_layer": (c_int, [c_void_p, c_char_p, T, c_int]),

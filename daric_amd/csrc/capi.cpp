@@ -3,6 +3,7 @@
 // (csrc/cache_ops/helpers.cu:15-174, copier.cpp:7-111, kernels.cu:127-330)
 // in the same order and with the same messages; no device work is enqueued
 // before every check has passed.
+#include <optional>
 #include <algorithm>
 #include <limits>
 #include <map>
@@ -947,7 +948,10 @@ int scatter_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs, 
         }
         DeviceGuard guard(r.device);
         const hipStream_t st = as_stream(stream);
-        uint8_t* scratch = staged > 0 ? noalloc_scratch(r.device) : nullptr;
+        // staged descriptors: this call's turn on the GPU's scratch array
+        std::optional<ScratchUse> use;
+        if (staged > 0) use.emplace(r.device, st);
+        uint8_t* scratch = use ? use->ptr() : nullptr;
         size_t scratch_off = 0;
         for (const Group& gr : groups) {
             if (gr.max_tiles == 0) continue;
@@ -982,6 +986,7 @@ int scatter_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs, 
             launch_scatter_rotate(ho.arg(), static_cast<int>(gr.jobs.size()), static_cast<int>(gr.max_tiles),
                                   gd, gr.kind, rope->is_neox != 0, rope->inv_freq, st);
         }
+        if (use) use->finish();
     });
 }
 

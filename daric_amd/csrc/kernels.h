@@ -1,6 +1,8 @@
 // Launchers of the gfx950 kernels (defined in the .hip files).
 #pragma once
 
+#include <mutex>
+
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
@@ -152,6 +154,29 @@ void launch_upload(const void* src, void* dst, size_t n16, hipStream_t stream);
 constexpr size_t kNoAllocScratchBytes = 256 * 1024;
 uint8_t* noalloc_scratch(int device);
 void stash_descriptors(const void* src, size_t bytes, uint8_t* dst, hipStream_t stream);
+
+// One call's use of a GPU's scratch array. The constructor takes the device's
+// call lock and, when the previous eager call used another stream, makes
+// `stream` wait for that call's last kernel; finish() is called after the
+// call's last launch that reads the array and records the device's event on
+// `stream`. Under stream capture neither the wait nor the record is made.
+struct ScratchState;
+class ScratchUse {
+public:
+    ScratchUse(int device, hipStream_t stream);
+    ScratchUse(const ScratchUse&) = delete;
+    ScratchUse& operator=(const ScratchUse&) = delete;
+    uint8_t* ptr() const;
+    void finish();
+
+private:
+    ScratchState* state_;
+    hipStream_t stream_;
+    std::unique_lock<std::mutex> lock_;
+    bool capture_ = false;
+};
+// Cross-stream waits ScratchUse has enqueued since the library was loaded.
+int64_t scratch_stream_waits();
 
 // Launch-configuration error check after a <<<>>> launch.
 void check_launch(const char* what);

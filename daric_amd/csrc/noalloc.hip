@@ -4,11 +4,17 @@
 // kernel arguments. No hipMalloc, hipHostMalloc or copy-engine transfer is
 // involved, so callers that may not allocate (stream capture, serving loops
 // with a fixed memory budget) can use it. Every call on one GPU shares that
-// GPU's array: calls that overlap on one GPU (different streams, or graphs
-// replayed concurrently) race on it.
+// GPU's array. Eager calls are ordered on it: a call's stash kernels wait
+// (hipStreamWaitEvent) for an event recorded after the previous call's last
+// kernel when the two calls use different streams, and calls of different
+// host threads enqueue one at a time. Calls recorded into a graph take no
+// part in that ordering: replays of such a graph that overlap another call
+// on the same GPU race on the array.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <map>
+#include <memory>
 #include <mutex>
 
 #include "common.h"
@@ -35,20 +41,73 @@ static_assert(kInlineDescBytes % 16 == 0 && kInlineDescBytes / 16 <= 256, "one s
 
 }  // namespace
 
-uint8_t* noalloc_scratch(int device) {
+// Per-GPU state of the scratch array, set up once per device with that
+// device current: the array's device address, and the event that completes
+// with the last kernel of the last eager call that read the array.
+struct ScratchState {
+    uint8_t* ptr = nullptr;
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;   // stream `done` was recorded on
+    bool recorded = false;
+    std::mutex call_mu;           // held by one call from its first stash to its record
+};
+
+namespace {
+
+std::atomic<int64_t> g_scratch_waits{0};
+
+ScratchState& scratch_state(int device) {
     static std::mutex mu;
-    static std::map<int, uint8_t*> ptrs;
+    static std::map<int, std::unique_ptr<ScratchState>> states;
     std::lock_guard<std::mutex> lk(mu);
-    auto it = ptrs.find(device);
-    if (it != ptrs.end()) return it->second;
-    DeviceGuard guard(device);   // the symbol's address on `device`
+    auto& s = states[device];
+    if (s) return *s;
+    std::unique_ptr<ScratchState> fresh(new ScratchState());
+    DeviceGuard guard(device);   // the symbol's address, and the event, on `device`
     void* p = nullptr;
     DARIC_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     DARIC_CHECK(p != nullptr && reinterpret_cast<uintptr_t>(p) % 256 == 0,
                 "scratch array has no usable device address on device ", device);
-    ptrs[device] = static_cast<uint8_t*>(p);
-    return static_cast<uint8_t*>(p);
+    fresh->ptr = static_cast<uint8_t*>(p);
+    DARIC_HIP_CHECK(hipEventCreateWithFlags(&fresh->done, hipEventDisableTiming));
+    s = std::move(fresh);
+    return *s;
 }
+
+// Whether work enqueued on `stream` is being recorded into a graph (an
+// unanswerable query counts as capturing: no event work is added then).
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;
+    }
+    return cs != hipStreamCaptureStatusNone;
+}
+
+}  // namespace
+
+uint8_t* noalloc_scratch(int device) { return scratch_state(device).ptr; }
+
+ScratchUse::ScratchUse(int device, hipStream_t stream)
+    : state_(&scratch_state(device)), stream_(stream), lock_(state_->call_mu) {
+    capture_ = capturing(stream);
+    if (!capture_ && state_->recorded && state_->last != stream) {
+        DARIC_HIP_CHECK(hipStreamWaitEvent(stream, state_->done, 0));
+        g_scratch_waits.fetch_add(1, std::memory_order_relaxed);
+    }
+}
+
+uint8_t* ScratchUse::ptr() const { return state_->ptr; }
+
+void ScratchUse::finish() {
+    if (capture_) return;
+    DARIC_HIP_CHECK(hipEventRecord(state_->done, stream_));
+    state_->last = stream_;
+    state_->recorded = true;
+}
+
+int64_t scratch_stream_waits() { return g_scratch_waits.load(std::memory_order_relaxed); }
 
 void stash_descriptors(const void* src, size_t bytes, uint8_t* dst, hipStream_t stream) {
     for (size_t off = 0; off < bytes; off += kInlineDescBytes) {

@@ -87,7 +87,13 @@ DescRing& DescRing::for_device(int device) {
     return *r;
 }
 
+namespace {
+std::atomic<int64_t> g_ring_uploads{0};
+std::atomic<int64_t> g_ring_allocations{0};
+}  // namespace
+
 void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* slot_out, bool direct) {
+    g_ring_uploads.fetch_add(1, std::memory_order_relaxed);
     // A slot between upload() and release() belongs to a call that is still
     // enqueueing kernels on it; skip such slots (wait if all are taken). The
     // lock covers only the choice of the slot: waiting for its previous
@@ -114,6 +120,7 @@ void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* s
             for (Slot& t : slots_) {
                 if (t.ev == nullptr) DARIC_HIP_CHECK(hipEventCreateWithFlags(&t.ev, hipEventDisableTiming));
                 if (t.cap == 0) {
+                    g_ring_allocations.fetch_add(1, std::memory_order_relaxed);
                     DARIC_HIP_CHECK(hipHostMalloc(&t.host, kInitialCap, hipHostMallocCoherent));
                     DARIC_HIP_CHECK(hipMalloc(&t.dev, kInitialCap));
                     t.cap = kInitialCap;
@@ -142,6 +149,7 @@ void* DescRing::upload(const void* src, size_t bytes, hipStream_t stream, int* s
             // Coherent (fine-grained) pinned memory: the upload kernel reads it
             // over the bus, so no stale GPU-cached copy of an earlier use of the
             // slot can be seen.
+            g_ring_allocations.fetch_add(1, std::memory_order_relaxed);
             DARIC_HIP_CHECK(hipHostMalloc(&s.host, cap, hipHostMallocCoherent));
             DARIC_HIP_CHECK(hipMalloc(&s.dev, cap));
             s.cap = cap;
@@ -222,6 +230,14 @@ const char* daric_last_error(void) { return daric::last_error(); }
 
 int daric_timing_enable(int enable) {
     return guarded([&] { g_timing.store(enable != 0); });
+}
+
+int daric_debug_counters(int64_t* descriptor_uploads, int64_t* ring_allocations, int64_t* scratch_waits) {
+    return guarded([&] {
+        if (descriptor_uploads) *descriptor_uploads = g_ring_uploads.load(std::memory_order_relaxed);
+        if (ring_allocations) *ring_allocations = g_ring_allocations.load(std::memory_order_relaxed);
+        if (scratch_waits) *scratch_waits = scratch_stream_waits();
+    });
 }
 
 int daric_timing_read(double* total_ms, int64_t* launches) {

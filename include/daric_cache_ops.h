@@ -99,6 +99,16 @@ const char* daric_last_error(void);
 int daric_timing_enable(int enable);
 int daric_timing_read(double* total_ms, int64_t* launches);
 
+/* Host-side counters since the library was loaded, for tests and monitoring
+ * (any pointer may be NULL): descriptor_uploads counts descriptor sets handed
+ * to the per-device descriptor ring (each copies into a pinned slot),
+ * ring_allocations the pinned/device buffer pairs the ring has allocated, and
+ * scratch_waits the cross-stream waits the allocation-free entry point has
+ * enqueued to order its calls on a GPU's scratch array. No counterpart in
+ * the reference. */
+int daric_debug_counters(int64_t* descriptor_uploads, int64_t* ring_allocations,
+                         int64_t* scratch_waits);
+
 /* ---------------------------------------------------------------------- */
 /* CacheCopier: reference csrc/cache_ops/cache_ops.h:91-125, copier.cpp   */
 /* ---------------------------------------------------------------------- */
@@ -188,12 +198,18 @@ int daric_copier_scatter_pages_rerotate(daric_copier* copier,
  * that it allocates on first use), this entry point stages it in a static
  * device array of 262144 bytes per GPU (3276 jobs of 80 bytes), carried there
  * by kernels whose arguments hold the bytes. It calls no hipMalloc, hipFree
- * or hipHostMalloc and enqueues only kernels. A call whose jobs need more
- * than the array holds, or whose layout needs the scatter-then-rotate form,
- * returns DARIC_ERR_INVALID before any device work.
+ * or hipHostMalloc and enqueues only kernels (plus, for staged job lists,
+ * one event record, and a stream wait when the stream changes; the event is
+ * created once per GPU, with the array's address, at the first staging call).
+ * A call whose jobs need more than the array holds, or whose layout needs the
+ * scatter-then-rotate form, returns DARIC_ERR_INVALID before any device work.
  * Every call on one GPU uses that GPU's array, which keeps the last call's
- * descriptors: calls that overlap on one GPU (on different streams, or
- * graphs replayed concurrently) race on it, and the caller must order them. */
+ * descriptors. Eager calls are ordered on it by the library: a call on
+ * another stream than the previous staging call waits for that call's
+ * kernels before it overwrites the array, and calls from different host
+ * threads enqueue one at a time. Calls recorded under stream capture add no
+ * such ordering: a graph replay that overlaps another call on the same GPU
+ * races on the array, and the caller must order those. */
 int daric_copier_scatter_pages_rerotate_noalloc(daric_copier* copier,
                                                 const char* const* layer_names, int64_t n_jobs,
                                                 const int64_t* offsets, int64_t n_offsets,

@@ -104,37 +104,52 @@ def test_layerwise_and_null_blocks(dev):
         assert same_bytes(fresh_dev[n], fresh_cpu[n])
 
 
-def test_load_rerotate_matches_oracle(dev):
-    names, cpu, pf, bpb, groups = setup(dev)
+@pytest.mark.parametrize("two_groups,layerwise,layout", [(False, False, "nhd"), (False, True, "nhd"),
+                                                          (True, False, "pf"), (True, True, "nhd")])
+def test_load_rerotate_matches_oracle(dev, two_groups, layerwise, layout):
+    """The fused load (records scattered and K moved from the saved position
+    to the new one in one pass) against the oracle's load then rotation:
+    whole records or one layer's record (the reference's per-layer load,
+    worker.py:219-231), one KV-cache group or two (each layer's pages are its
+    group's block list)."""
+    names, cpu, pf, bpb, groups = setup(dev, n_layers=4, layout=layout, two_groups=two_groups)
     rng = np.random.default_rng(3)
-    blocks = metas_blocks(rng, 5, 64, False)
+    blocks = metas_blocks(rng, 5, 64, two_groups)
     host = torch.zeros(32 << 20, dtype=torch.uint8, pin_memory=True)
     shm = torch.zeros(32 << 20, dtype=torch.uint8)
     dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
-    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, dev_caches, host, staging_bytes=640 << 10)
+    L = len(names)
+    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * L, dev_caches, host, staging_bytes=640 << 10)
     offs, _ = record_offsets(ctx, blocks)
     saved = [0, 512, 77, 3000, 9]
-    ctx.store(offs, blocks, saved)
-    okv.OracleKVIO(names, groups, bpb, [pf] * 3, cpu, shm).store(offs, blocks, saved)
+    layer = names[2] if layerwise else None
+    ctx.store(offs, blocks, saved, layer_name=layer)
+    okv.OracleKVIO(names, groups, bpb, [pf] * L, cpu, shm).store(offs, blocks, saved, layer_name=layer)
     assert torch.equal(host, shm)
     R = 64
     inv = orope.default_inv_freq(R, 500000.0)
     new_pos = [100, 512, 4000, 0, 20000]
-    ntok = [len(b[0]) * 16 - 3 for b in blocks]
+    # tokens per meta: within the shorter group's pages when there are two
+    ntok = [min(len(g) for g in b) * 16 - 3 for b in blocks]
     fresh_cpu = {n: torch.zeros_like(t) for n, t in cpu.items()}
     fresh_dev = {n: to_dev(t, dev) for n, t in fresh_cpu.items()}
-    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, fresh_dev, host, staging_bytes=640 << 10)
-    ctx2.load(offs, blocks, rerotate=(new_pos, ntok, torch.from_numpy(inv).to(dev), R, True))
+    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * L, fresh_dev, host, staging_bytes=640 << 10)
+    got = ctx2.load(offs, blocks, layer_name=layer,
+                    rerotate=(new_pos, ntok, torch.from_numpy(inv).to(dev), R, True))
     torch.cuda.synchronize()
-    okv.OracleKVIO(names, groups, bpb, [pf] * 3, fresh_cpu, shm).load(
-        offs, blocks, rerotate=(new_pos, ntok, inv, R, True))
-    slots = []
-    for b, nt, np_, sp in zip(blocks, ntok, new_pos, saved):
-        if np_ != sp:
-            slots += [b[0][j // 16] * 16 + j % 16 for j in range(nt)]
-    for n in names:
+    want = okv.OracleKVIO(names, groups, bpb, [pf] * L, fresh_cpu, shm).load(
+        offs, blocks, layer_name=layer, rerotate=(new_pos, ntok, inv, R, True))
+    assert got == want == saved
+    for n, gi in zip(names, groups):
+        slots = []
+        if layer is None or n == layer:
+            for b, nt, np_, sp in zip(blocks, ntok, new_pos, saved):
+                if np_ != sp:
+                    slots += [b[gi][j // 16] * 16 + j % 16 for j in range(nt)]
         mask, pn = rotation_region(fresh_cpu[n], pf, R, slots, True)
         assert_rotation_parity(fresh_dev[n], fresh_cpu[n], mask, pn)
+        if layer is not None and n != layer:
+            assert not bool(fresh_dev[n].view(torch.int16).any()), f"layer {n} was not loaded"
 
 
 def test_store_and_load_from_two_threads(dev):
@@ -240,13 +255,36 @@ if KV_FUZZ is not None:
         fresh_cpu = {n: torch.zeros_like(t) for n, t in cpu.items()}
         fresh_dev = {n: to_dev(t, dev) for n, t in fresh_cpu.items()}
         ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * n_layers, fresh_dev, host, staging_bytes=1 << 20)
-        got = ctx2.load(offs, load_blocks, layer_name=layer_name)
+        # the fused re-rotating load: K of each meta's first tokens moved from
+        # the saved position to a drawn one
+        rerot = None
+        if data.draw(st.booleans(), label="rerotate"):
+            R = data.draw(st.sampled_from([16, 32, 64]), label="rotary_dim")
+            neox = data.draw(st.booleans(), label="neox")
+            new_pos = [int(saved[k]) + int(d) for k, d in enumerate(rng.integers(-5000, 5000, n_meta))]
+            if n_meta > 1:
+                new_pos[1] = saved[1]                       # a meta that does not move
+            ntok = [int(rng.integers(0, min(len(g) for g in b) * 16 + 1)) for b in load_blocks]
+            inv = orope.default_inv_freq(R, 500000.0)
+            rerot = (new_pos, ntok, inv, R, neox)
+        got = ctx2.load(offs, load_blocks, layer_name=layer_name,
+                        rerotate=None if rerot is None else
+                        (rerot[0], rerot[1], torch.from_numpy(rerot[2]).to(dev), rerot[3], rerot[4]))
         torch.cuda.synchronize()
         want = okv.OracleKVIO(names, groups, bpb, [pf] * n_layers, fresh_cpu, shm).load(
-            offs, load_blocks, layer_name=layer_name)
+            offs, load_blocks, layer_name=layer_name, rerotate=rerot)
         assert got == want == saved
-        for n in names:
-            assert same_bytes(fresh_dev[n], fresh_cpu[n])
+        for n, gi in zip(names, groups):
+            if rerot is None:
+                assert same_bytes(fresh_dev[n], fresh_cpu[n])
+                continue
+            slots = []
+            if layer_name is None or n == layer_name:
+                for b, nt, npos, sp in zip(load_blocks, rerot[1], rerot[0], saved):
+                    if npos != sp:
+                        slots += [b[gi][j // 16] * 16 + j % 16 for j in range(nt) if b[gi][j // 16] != 0]
+            mask, pn = rotation_region(fresh_cpu[n], pf, rerot[3], slots, rerot[4])
+            assert_rotation_parity(fresh_dev[n], fresh_cpu[n], mask, pn)
 
 
 def test_concurrent_stores_take_turns_and_close_drains(dev):

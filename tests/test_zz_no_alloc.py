@@ -4,7 +4,11 @@ against the existing entry point (daric_copier_scatter_pages_rerotate) on
 the same inputs: bit-exact, on calls in a row whose job lists shrink (the
 static scratch array keeps the previous call's descriptors), with two launch
 groups staged in one call, and with a job list small enough to travel in the
-kernel arguments. Device memory stays unallocated across the calls."""
+kernel arguments. Device memory stays unallocated across the calls, and the
+library's own counters show that no call touches the descriptor ring (whose
+slots are pinned host and device allocations), the first call included.
+Calls on two streams in a row, with different job lists, are ordered on the
+shared scratch array by the library and stay bit-exact."""
 import ctypes
 
 import numpy as np
@@ -49,6 +53,12 @@ def call(lib, fn, copier, names, offsets, sizes, idx, ioff, deltas, ntok, rope, 
     ix = _lib.desc(idx)
     return fn(copier._h, _lib.str_array(names), len(names), off.ptr, off.n, sz.ptr, sz.n,
               ctypes.byref(ix), io.ptr, io.n, dl.ptr, nt.ptr, ctypes.byref(rope), ctypes.c_uint64(stream))
+
+
+def counters(lib):
+    up, al, wt = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    assert lib.daric_debug_counters(ctypes.byref(up), ctypes.byref(al), ctypes.byref(wt)) == 0
+    return up.value, al.value, wt.value
 
 
 def test_noalloc_matches_fused_entry_point(dev):
@@ -97,9 +107,11 @@ def test_noalloc_matches_fused_entry_point(dev):
         # first launch there took 2 MiB of device memory on MI355X); the later
         # calls must take none: the ring's device half alone would be 16 MiB.
         free_before = torch.cuda.mem_get_info()[0]
+        ring_before = counters(lib)[:2]
         st = call(lib, lib.daric_copier_scatter_pages_rerotate_noalloc, copiers[1], names, offsets, sizes,
                   idx, ioff, deltas, ntok, rope, side.cuda_stream)
         assert st == 0, lib.daric_last_error()
+        assert counters(lib)[:2] == ring_before, f"call {k} used the descriptor ring"
         torch.cuda.synchronize()
         if k > 0:
             assert torch.cuda.mem_get_info()[0] == free_before, f"call {k} took device memory"
@@ -107,3 +119,58 @@ def test_noalloc_matches_fused_entry_point(dev):
             assert same_bytes(outs[1][l], outs[0][l]), f"call {k} layer {l}"
     # both paths really rotated something
     assert not same_bytes(outs[0][0], base[0])
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(dev):
+    """Two calls in a row on different streams, each staging its own job list
+    in the same region of the scratch array, then a third back on the first
+    stream: the second call's stash waits for the first call's kernel (and
+    the third for the second's), so every call rotates with its own
+    descriptors. Each result is bit-exact against the regular entry point."""
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(11)
+    rng = np.random.default_rng(11)
+    dims = [128] * 8
+    span_of = lambda l: PS * H * dims[l] * 2
+    inv = (1.0 / (500000.0 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).to(dev)
+    rope = _lib.DaricRope()
+    rope.inv_freq = inv.data_ptr()
+    rope.rotary_dim = 128
+    rope.is_neox = 1
+    perm = (rng.permutation(NB - 1) + 1).tolist()
+    # 10 x 8 = 80 jobs (6400 descriptor bytes, staged), 6 x 8 = 48 (staged), 8 x 8 = 64 (staged)
+    job_lists = [[perm[4 * i: 4 * i + 4] for i in range(10)],
+                 [perm[40 + 3 * i: 43 + 3 * i] for i in range(6)],
+                 [perm[60 + 2 * i: 62 + 2 * i] for i in range(8)]]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    which = [0, 1, 0]
+    cases = []
+    for chunks in job_lists:
+        names, offsets, sizes, flat, ioff, deltas, ntok, total = plan(len(dims), chunks, span_of, rng)
+        staging = torch.randint(-128, 127, (total,), dtype=torch.int8, generator=gen).view(torch.uint8).to(dev)
+        idx = torch.tensor(flat, dtype=torch.int32, device=dev)
+        base = make_layers(dev, dims, gen)
+        pair = []
+        for _ in range(2):
+            c = cache_ops.CacheCopier()
+            layers = [t.clone() for t in base]
+            for l, t in enumerate(layers):
+                c.register_layer(f"model.layers.{l}.self_attn.attn", t, False)
+            c.register_store(staging)
+            pair.append((c, layers))
+        cases.append((pair, (names, offsets, sizes, idx, ioff, deltas, ntok), base))
+    torch.cuda.synchronize()
+    for pair, args, _ in cases:
+        assert call(lib, lib.daric_copier_scatter_pages_rerotate, pair[0][0], *args, rope,
+                    torch.cuda.current_stream().cuda_stream) == 0, lib.daric_last_error()
+    torch.cuda.synchronize()
+    waits0 = counters(lib)[2]
+    for (pair, args, _), s in zip(cases, which):
+        assert call(lib, lib.daric_copier_scatter_pages_rerotate_noalloc, pair[1][0], *args, rope,
+                    streams[s].cuda_stream) == 0, lib.daric_last_error()
+    torch.cuda.synchronize()
+    assert counters(lib)[2] - waits0 == 2, "each stream change waits for the previous call"
+    for k, (pair, _, base) in enumerate(cases):
+        for l in range(len(dims)):
+            assert same_bytes(pair[1][1][l], pair[0][1][l]), f"call {k} layer {l}"
+        assert not same_bytes(pair[0][1][0], base[0])
