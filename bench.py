@@ -249,8 +249,11 @@ def config3_inputs(dev, seed=0):
 
 def run_config3(steps, warmup, seed=0):
     """Batched selective recompute (config3_inputs). One
-    step = kv_deviation + topk_per_chunk (k = 77 of 512) + merge_rows of the
-    selected K/V rows."""
+    step = select_merge: the deviation keys, the top-k (k = 77 of 512) and the
+    merge of the selected K/V rows (the deviation kernel, then one workgroup
+    per (layer, chunk) for top-k and merge). The same work as three calls
+    (kv_deviation, topk_per_chunk, merge_rows) and as one launch is timed
+    beside it."""
     from daric_amd import cache_ops
     dev = torch.device("cuda:0")
     w = config3_inputs(dev, seed)
@@ -270,14 +273,32 @@ def run_config3(steps, warmup, seed=0):
     def merge_step():
         cache_ops.merge_rows(layers, False, bt, k_new, v_new, chunks, sel, stream=st)
 
-    def step():
+    def three_calls():
         dev_step()
         topk_step()
         merge_step()
 
+    def step():
+        # the library's selection call: the deviation kernel, then one
+        # workgroup per (layer, chunk) for the chunk's top-k and merge
+        cache_ops.select_merge(layers, False, bt, k_new, v_new, chunks, kmax=k, keys=keys, sel_idx=sel, stream=st)
+
+    def one_pass():
+        cache_ops.select_merge(layers, False, bt, k_new, v_new, chunks, kmax=k, keys=keys, sel_idx=sel, stream=st,
+                               one_pass=True)
+
     whole = time_steps(step, steps, warmup, stream)
+    # the three forms alternately, three rounds each: medians
+    forms = {"select_merge": [], "three_calls": [], "one_pass": []}
+    for _ in range(3):
+        for name, f in (("select_merge", step), ("three_calls", three_calls), ("one_pass", one_pass)):
+            forms[name].append(time_steps(f, steps, 1, stream)["step_ms"])
+    forms = {n: sorted(v)[1] for n, v in forms.items()}
     parts = {n: time_steps(f, steps, 1, stream)["kern_ms"]
-             for n, f in (("deviation", dev_step), ("topk", topk_step), ("merge", merge_step))}
+             for n, f in (("deviation", dev_step), ("topk", topk_step), ("merge", merge_step),
+                          ("topk_merge_fused", lambda: cache_ops.select_merge(
+                              layers, False, bt, k_new, v_new, chunks, kmax=k, keys=keys, sel_idx=sel, stream=st,
+                              keys_ready=True)))}
     # The merge's address pattern in isolation: the same kernel moving the
     # same rows' worth of bytes, but with each chunk's first k tokens selected
     # and chunks laid on consecutive blocks, so both the recomputed rows read
@@ -318,9 +339,17 @@ def run_config3(steps, warmup, seed=0):
                tokens=T, k=k, ms_per_step=whole["step_ms"], tokens_per_s=T / (whole["step_ms"] / 1e3),
                algorithmic_bytes=total, GBps=_gbps(total, whole["step_ms"]),
                frac=_gbps(total, whole["step_ms"]) / PEAK_HBM_GBPS,
+               step_forms=dict(
+                   ms=forms, note="the same selection, same process, alternating (median of 3): select_merge "
+                                  "(deviation kernel, then one workgroup per (layer, chunk) for top-k and "
+                                  "merge; the step above), three_calls (kv_deviation, topk_per_chunk, "
+                                  "merge_rows), one_pass (one launch: each workgroup also computes its "
+                                  "chunk's keys)"),
                kernels={"deviation": dict(ms=parts["deviation"], bytes=dev_bytes,
                                           GBps=_gbps(dev_bytes, parts["deviation"])),
                         "topk": dict(ms=parts["topk"], bytes=topk_bytes),
+                        "topk_merge_fused": dict(ms=parts["topk_merge_fused"], bytes=topk_bytes + merge_bytes,
+                                                 GBps=_gbps(topk_bytes + merge_bytes, parts["topk_merge_fused"])),
                         "merge": dict(ms=parts["merge"], bytes=merge_bytes,
                                       GBps=_gbps(merge_bytes, parts["merge"]),
                                       frac=_gbps(merge_bytes, parts["merge"]) / PEAK_HBM_GBPS,
@@ -689,14 +718,30 @@ def run_config5(steps, warmup, seed=0):
         cache_ops.merge_rows(cache, False, bt, k_new, v_new, chunks, sel, stream=st, k_scales=k_scales,
                              v_scales=v_scales)
 
-    def sel_step():
+    def three_calls():
         dev_step()
         topk_step()
         merge_step()
 
+    def sel_step():
+        cache_ops.select_merge(cache, False, bt, k_new, v_new, chunks, kmax=k, keys=keys, sel_idx=sel, stream=st,
+                               k_scales=k_scales, v_scales=v_scales)
+
+    def one_pass():
+        cache_ops.select_merge(cache, False, bt, k_new, v_new, chunks, kmax=k, keys=keys, sel_idx=sel, stream=st,
+                               k_scales=k_scales, v_scales=v_scales, one_pass=True)
+
     selection = time_steps(sel_step, steps, warmup, stream)
+    forms = {"select_merge": [], "three_calls": [], "one_pass": []}
+    for _ in range(3):
+        for name, f in (("select_merge", sel_step), ("three_calls", three_calls), ("one_pass", one_pass)):
+            forms[name].append(time_steps(f, steps, 1, stream)["step_ms"])
+    forms = {n: sorted(v)[1] for n, v in forms.items()}
     parts = {n: time_steps(f, steps, 1, stream)["kern_ms"]
-             for n, f in (("deviation", dev_step), ("topk", topk_step), ("merge", merge_step))}
+             for n, f in (("deviation", dev_step), ("topk", topk_step), ("merge", merge_step),
+                          ("topk_merge_fused", lambda: cache_ops.select_merge(
+                              cache, False, bt, k_new, v_new, chunks, kmax=k, keys=keys, sel_idx=sel, stream=st,
+                              k_scales=k_scales, v_scales=v_scales, keys_ready=True)))}
     dev_bytes = T * L * H * D * (2 + 1) + T * L * 4
     topk_bytes = T * L * 4 + C * L * k * 4
     merge_bytes = C * k * L * 2 * (H * D * (2 + 1))      # bf16 rows read, e4m3 codes written
@@ -712,9 +757,15 @@ def run_config5(steps, warmup, seed=0):
                                  fused_frac_of_it=pattern["kern_ms"] / fused["kern_ms"]),
                selection=dict(k=k, ms_per_step=selection["step_ms"], algorithmic_bytes=sel_bytes,
                               GBps=_gbps(sel_bytes, selection["step_ms"]),
+                              step_forms=dict(ms=forms, note="as for config 3: select_merge (the step above), "
+                                                             "three_calls, one_pass; alternating, median of 3"),
                               kernels={"deviation": dict(ms=parts["deviation"], bytes=dev_bytes,
                                                          GBps=_gbps(dev_bytes, parts["deviation"])),
                                        "topk": dict(ms=parts["topk"], bytes=topk_bytes),
+                                       "topk_merge_fused": dict(ms=parts["topk_merge_fused"],
+                                                                bytes=topk_bytes + merge_bytes,
+                                                                GBps=_gbps(topk_bytes + merge_bytes,
+                                                                           parts["topk_merge_fused"])),
                                        "merge_quantising": dict(ms=parts["merge"], bytes=merge_bytes,
                                                                 GBps=_gbps(merge_bytes, parts["merge"]))}))
     del w, cache, cp, k_new, v_new, keys, sel

@@ -95,6 +95,8 @@ SIGNATURES = {
     "daric_kv_deviation": (c_int, [T, c_int64, c_int, T, T, P(DaricChunk), c_int64, T, T, c_uint64]),
     "daric_topk_per_chunk": (c_int, [T, P(DaricChunk), c_int64, T, c_uint64]),
     "daric_merge_rows": (c_int, [T, c_int64, c_int, T, T, T, P(DaricChunk), c_int64, T, T, T, c_uint64]),
+    "daric_select_merge": (c_int, [T, c_int64, c_int, T, T, T, P(DaricChunk), c_int64, T, T, T, T, c_int,
+                                   c_uint64]),
 }
 
 _lib = None

@@ -388,6 +388,55 @@ def merge_rows(layers: Sequence[torch.Tensor], page_first: bool, block_table: to
     _record(st, dev, block_table, k_new, v_new, sel_idx, k_scales, v_scales)
 
 
+SELECT_KEYS_READY = 1       # DARIC_SELECT_KEYS_READY
+SELECT_ONE_PASS = 2         # DARIC_SELECT_ONE_PASS
+
+
+def select_merge(layers: Sequence[torch.Tensor], page_first: bool, block_table: torch.Tensor,
+                 k_new: torch.Tensor, v_new: Optional[torch.Tensor], chunks, kmax: Optional[int] = None,
+                 keys: Optional[torch.Tensor] = None, sel_idx: Optional[torch.Tensor] = None,
+                 keys_ready: bool = False, k_scales: Optional[torch.Tensor] = None,
+                 v_scales: Optional[torch.Tensor] = None, stream: int = 0, one_pass: bool = False):
+    """kv_deviation + topk_per_chunk + merge_rows in one call: returns
+    (keys [L, T] fp32, sel_idx [L, n_chunks, kmax] int32), equal to what the
+    three calls return, and merges the selected rows the same way. Where the
+    chunks fit, the top-k and merge run fused, one workgroup per (layer,
+    chunk). For an fp8 cache, k_scales / v_scales are its [L, H] per-head K / V
+    scales. keys_ready: `keys` already holds the deviation keys. one_pass: the
+    fused workgroups compute the keys too (one launch; measured slower)."""
+    layers = list(layers)
+    dev = layers[0].device
+    st = _resolve_stream(stream, dev)
+    ch = list(chunks) if not isinstance(chunks, np.ndarray) else chunks.tolist()
+    if kmax is None:
+        kmax = max([min(int(c[3]), int(c[2])) for c in ch] + [0])
+    carr, n, _keep = _chunks(ch)
+    shape = (len(layers), k_new.shape[1])
+    if keys is None:
+        if keys_ready:
+            raise ValueError("keys_ready needs keys")
+        # zeroed on the launch stream: rows outside every chunk stay 0
+        with torch.cuda.stream(_ext_stream(st, dev)):
+            keys = torch.zeros(shape, dtype=torch.float32, device=dev)
+    if sel_idx is None:
+        with torch.cuda.stream(_ext_stream(st, dev)):
+            sel_idx = torch.empty(len(layers), n, kmax, dtype=torch.int32, device=dev)
+    bt, kn, kd, si = desc(block_table), desc(k_new), desc(keys), desc(sel_idx)
+    vn = desc(v_new) if v_new is not None else None
+    ks = desc(k_scales) if k_scales is not None else None
+    vs = desc(v_scales) if v_scales is not None else None
+    check(load().daric_select_merge(_layer_array(layers), len(layers), 1 if page_first else 0,
+                                    ctypes.byref(bt), ctypes.byref(kn),
+                                    ctypes.byref(vn) if vn is not None else None, carr, n,
+                                    ctypes.byref(ks) if ks is not None else None,
+                                    ctypes.byref(vs) if vs is not None else None,
+                                    ctypes.byref(kd), ctypes.byref(si),
+                                    (SELECT_KEYS_READY if keys_ready else 0) | (SELECT_ONE_PASS if one_pass else 0),
+                                    ctypes.c_uint64(st)))
+    _record(st, dev, block_table, k_new, v_new, keys, sel_idx, k_scales, v_scales)
+    return keys, sel_idx
+
+
 def timing_enable(enable: bool = True) -> None:
     check(load().daric_timing_enable(1 if enable else 0))
 

@@ -1317,4 +1317,116 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
     });
 }
 
+int daric_select_merge(const daric_tensor* layers, int64_t n_layers, int page_first,
+                       const daric_tensor* block_table, const daric_tensor* k_new, const daric_tensor* v_new,
+                       const daric_chunk* chunks, int64_t n_chunks, const daric_tensor* k_scales,
+                       const daric_tensor* v_scales, daric_tensor* keys, daric_tensor* sel_idx,
+                       int flags, uint64_t stream) {
+    return guarded([&] {
+        DARIC_CHECK(n_layers > 0 && layers != nullptr, "layers must not be empty");
+        for (int64_t i = 0; i < n_layers; ++i) check_tensor_struct(&layers[i], "kv layer");
+        check_same_layers(layers, n_layers);
+        const daric_tensor& t = layers[0];
+        DARIC_CHECK(t.device >= 0, "KV cache tensor must be on CUDA");
+        const int ck = elem_kind(t);
+        DARIC_CHECK(ck >= 0, "unsupported KV cache dtype for select_merge");
+        const KVGeom g = kv_geom(t, page_first != 0);
+        check_block_table(block_table, t.device);
+        int64_t T = 0, Tv = 0;
+        check_rows_tensor(k_new, t, n_layers, g.H, g.D, "k_new", &T);
+        const int nk = k_new->dtype == DARIC_DTYPE_BFLOAT16 ? kBF16 : (k_new->dtype == DARIC_DTYPE_FLOAT16 ? kF16 : -1);
+        DARIC_CHECK(nk >= 0, "k_new must be bfloat16 or float16");
+        DARIC_CHECK((flags & ~(DARIC_SELECT_KEYS_READY | DARIC_SELECT_ONE_PASS)) == 0, "unknown select_merge flags ",
+                    flags);
+        const bool keys_ready = (flags & DARIC_SELECT_KEYS_READY) != 0;
+        const bool one_pass = !keys_ready && (flags & DARIC_SELECT_ONE_PASS) != 0;
+        const bool quant = ck == kE4M3;
+        DARIC_CHECK(quant || k_new->dtype == t.dtype,
+                    "k_new must have the cache's element type, or be bfloat16/float16 rows for an fp8 "
+                    "(e4m3) cache");
+        if (g.v_off >= 0) {
+            check_rows_tensor(v_new, t, n_layers, g.H, g.D, "v_new", &Tv);
+            DARIC_CHECK(Tv == T && v_new->dtype == k_new->dtype && v_new->elem_size == k_new->elem_size,
+                        "v_new must match k_new");
+        }
+        const auto check_scales = [&](const daric_tensor* sc, const char* what) {
+            DARIC_CHECK(sc != nullptr && sc->data != nullptr, "selecting and merging ", quant_name(nk),
+                        " rows on an fp8 cache needs ", what);
+            check_tensor_struct(sc, what);
+            DARIC_CHECK(sc->device == t.device && sc->dtype == DARIC_DTYPE_FLOAT32 && is_contiguous(*sc) &&
+                        numel(*sc) == n_layers * g.H,
+                        what, " must be a contiguous float32 [n_layers, H] tensor on the layers' device");
+        };
+        if (quant) {
+            check_scales(k_scales, "k_scales");
+            if (g.v_off >= 0) check_scales(v_scales, "v_scales");
+            DARIC_CHECK(merge_fits_rows(g, t.elem_size, true),
+                        "quantising merge needs head_dim % 8 == 0, 8-byte aligned cache rows and K+V "
+                        "rows of at most ", merge_max_row_bytes() / 1024, " KiB of recomputed values per token");
+        } else {
+            DARIC_CHECK((k_scales == nullptr || k_scales->data == nullptr) &&
+                        (v_scales == nullptr || v_scales->data == nullptr),
+                        "k_scales / v_scales apply only to an fp8 cache");
+        }
+        const int64_t ces = t.elem_size;
+        const int64_t need = quant ? 8 : 16;
+        DARIC_CHECK(g.D % 8 == 0 && (g.sb * ces) % need == 0 && (g.ss * ces) % need == 0 &&
+                    (g.sh * ces) % need == 0 && (g.v_off < 0 || (g.v_off * ces) % need == 0),
+                    "select_merge needs head_dim % 8 == 0 and aligned K/V rows");
+        for (int64_t i = 0; i < n_layers; ++i) DARIC_CHECK(aligned(layers[i].data, need), "misaligned layer ", i);
+        check_tensor_struct(keys, "keys");
+        DARIC_CHECK(keys->device == t.device && keys->dtype == DARIC_DTYPE_FLOAT32 && keys->ndim == 2 &&
+                    keys->sizes[0] == n_layers && keys->sizes[1] == T && is_contiguous(*keys),
+                    "keys must be a contiguous float32 [n_layers, T] tensor");
+        check_tensor_struct(sel_idx, "sel_idx");
+        DARIC_CHECK(sel_idx->device == t.device && sel_idx->dtype == DARIC_DTYPE_INT32 &&
+                    sel_idx->ndim == 3 && sel_idx->sizes[0] == n_layers &&
+                    sel_idx->sizes[1] == n_chunks && is_contiguous(*sel_idx),
+                    "sel_idx must be a contiguous int32 [n_layers, n_chunks, kmax] tensor");
+        const int64_t kmax = sel_idx->sizes[2];
+        Chunks c = build_chunks(chunks, n_chunks, g.PS, numel(*block_table), T, deviation_tile_tokens(ck));
+        DARIC_CHECK(c.max_k <= kmax, "sel_idx kmax (", kmax, ") is smaller than a chunk's k (", c.max_k, ")");
+        DARIC_CHECK(c.tiles <= kMaxTiles && n_chunks <= kMaxTiles, "too many tokens in one select_merge call");
+        if (c.tiles == 0 && kmax == 0) return;   // no tokens to read, no index rows to fill
+        DeviceGuard guard(t.device);
+        const hipStream_t st = as_stream(stream);
+        const size_t cb = c.v.size() * sizeof(SelChunk);
+        std::vector<uint8_t> blob(cb + n_layers * sizeof(uint8_t*));
+        std::memcpy(blob.data(), c.v.data(), cb);
+        const auto ptrs = layer_ptrs(layers, n_layers);
+        std::memcpy(blob.data() + cb, ptrs.data(), n_layers * sizeof(uint8_t*));
+        DescHandOver ho(t.device, blob.data(), blob.size(), st);
+        const float* ksc = quant ? static_cast<const float*>(k_scales->data) : nullptr;
+        const float* vsc = quant && g.v_off >= 0 ? static_cast<const float*>(v_scales->data) : nullptr;
+        float* kd = static_cast<float*>(keys->data);
+        int32_t* sd = static_cast<int32_t*>(sel_idx->data);
+        const auto* kn = static_cast<const uint8_t*>(k_new->data);
+        const auto* vn = g.v_off >= 0 ? static_cast<const uint8_t*>(v_new->data) : nullptr;
+        const auto* btp = static_cast<const int32_t*>(block_table->data);
+        if (kmax > 0 && select_merge_fits(g, t.elem_size, quant, c.max_tokens, kmax, one_pass)) {
+            // the keys by the deviation kernel (unless given, or one_pass), then
+            // one workgroup per (layer, chunk) for its top-k and merge
+            if (!keys_ready && !one_pass && c.tiles > 0)
+                launch_deviation(ho.arg(), static_cast<int>(cb), static_cast<int>(n_layers), g, ck, btp, kn, nk, T,
+                                 static_cast<int>(n_chunks), static_cast<int>(c.tiles), quant ? ksc : nullptr, kd,
+                                 st);
+            launch_select_merge(ho.arg(), static_cast<int>(cb), static_cast<int>(n_layers), g, ck, t.elem_size, btp,
+                                kn, nk, vn, T, static_cast<int>(n_chunks), static_cast<int>(c.max_tokens), one_pass,
+                                kd, sd, static_cast<int>(kmax), quant, ksc, vsc, st);
+            return;
+        }
+        // the same work as three launches (chunks longer than the fused
+        // kernel's LDS holds, or rows it does not take)
+        if (!keys_ready && c.tiles > 0)
+            launch_deviation(ho.arg(), static_cast<int>(cb), static_cast<int>(n_layers), g, ck, btp, kn, nk, T,
+                             static_cast<int>(n_chunks), static_cast<int>(c.tiles), quant ? ksc : nullptr, kd, st);
+        if (kmax == 0) return;
+        launch_topk(kd, static_cast<int>(n_layers), T, ho.arg(), static_cast<int>(n_chunks),
+                    static_cast<int>(std::max<int64_t>(c.max_tokens, 1)), sd, static_cast<int>(kmax), st);
+        if (c.max_k == 0) return;
+        launch_merge(ho.arg(), static_cast<int>(cb), static_cast<int>(n_layers), g, t.elem_size, btp, kn, vn, T,
+                     static_cast<int>(n_chunks), sd, static_cast<int>(kmax), quant ? nk : -1, ksc, vsc, st);
+    });
+}
+
 }  // extern "C"

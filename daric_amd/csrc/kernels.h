@@ -141,6 +141,20 @@ void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g
                   const int32_t* block_table, const uint8_t* k_new, const uint8_t* v_new,
                   int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, int quant_from,
                   const float* k_scales, const float* v_scales, hipStream_t stream);
+// Fused selection, one workgroup per (layer, chunk): top-k on the chunk's
+// keys held in LDS and the merge of its selected rows, with (with_keys) or
+// without (keys already hold them) the chunk's deviation keys computed first
+// in the same workgroup. select_merge_fits: whether it takes the geometry and
+// chunk sizes, and (unless one_pass) whether a chunk's selected rows are few
+// enough for one workgroup to merge faster than the merge kernel (else the
+// three launches above do the same work).
+bool select_merge_fits(const KVGeom& g, int elem_size, bool quant, int64_t max_tokens, int64_t kmax,
+                       bool one_pass);
+void launch_select_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g, int cache_kind,
+                         int elem_size, const int32_t* block_table, const uint8_t* k_new, int new_kind,
+                         const uint8_t* v_new, int64_t T, int n_chunks, int max_tokens, bool with_keys,
+                         float* keys, int32_t* sel_idx, int kmax, bool quant, const float* k_scales,
+                         const float* v_scales, hipStream_t stream);
 
 // Copies n16 16-byte units from host-pinned `src` to device `dst` on `stream`
 // (descriptor upload; both 16-byte aligned).

@@ -352,6 +352,31 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
                      const daric_tensor* k_scales, const daric_tensor* v_scales,
                      uint64_t stream);
 
+/* The whole recompute selection in one call: daric_kv_deviation (unless
+ * flags has DARIC_SELECT_KEYS_READY: keys already hold the keys), then
+ * daric_topk_per_chunk into sel_idx, then daric_merge_rows of the selected
+ * rows, with the same arguments, checks and results (keys, sel_idx and the
+ * merged cache bytes equal those of the three calls). For an fp8 (e4m3)
+ * cache, k_scales are the cache's per-(layer, head) K scales (they
+ * dequantise the cached K for the keys and quantise the merged K rows) and
+ * v_scales the V scales; k_new and v_new are bfloat16 or float16 rows. Other
+ * caches take rows of their own type and NULL scales.
+ * Chunks of up to 8192 tokens whose rows the merge kernel takes: the keys
+ * come from the deviation kernel, then one workgroup per (layer, chunk) runs
+ * the chunk's top-k on its keys in LDS and merges the selected rows, with no
+ * index round trip through memory. DARIC_SELECT_ONE_PASS computes the keys
+ * in that workgroup too (one launch; it measured 4-7% slower on MI355X at
+ * the Llama-3-8B and -70B selection workloads, and is kept for measurement).
+ * Other calls run the three kernels in turn. New entry point; no counterpart
+ * in the reference. */
+#define DARIC_SELECT_KEYS_READY 1
+#define DARIC_SELECT_ONE_PASS 2
+int daric_select_merge(const daric_tensor* layers, int64_t n_layers, int page_first,
+                       const daric_tensor* block_table, const daric_tensor* k_new,
+                       const daric_tensor* v_new, const daric_chunk* chunks, int64_t n_chunks,
+                       const daric_tensor* k_scales, const daric_tensor* v_scales,
+                       daric_tensor* keys, daric_tensor* sel_idx, int flags, uint64_t stream);
+
 #ifdef __cplusplus
 }
 #endif

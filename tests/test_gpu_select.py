@@ -277,3 +277,108 @@ def test_selection_over_more_than_65535_chunks(dev):
     torch.cuda.synchronize()
     osel.merge_rows([layer], False, bt, k_new, v_new, chunks, sel_o)
     assert same_bytes(gl[0], layer)
+
+
+def _oracle_selection(cpu, pf, bt, k_new, v_new, chunks, kmax, ks=None, vs=None):
+    keys = osel.deviation(cpu, pf, bt, k_new, chunks, k_scales=ks)
+    sel = osel.topk_per_chunk(keys, chunks, kmax)
+    osel.merge_rows(cpu, pf, bt, k_new, v_new, chunks, sel, k_scales=ks, v_scales=vs)
+    return keys, sel
+
+
+@pytest.mark.parametrize("layout", ["nhd", "hnd", "pf", "packed", "mla"])
+@pytest.mark.parametrize("mode", ["default", "keys_ready", "one_pass"])
+def test_select_merge_matches_oracle(dev, layout, mode):
+    """The whole selection in one call (the deviation kernel, then one
+    workgroup per (layer, chunk) for top-k and merge; keys_ready: keys from an
+    earlier kv_deviation; one_pass: those workgroups compute the keys too):
+    keys, indices and merged bytes bit-exact against the oracle's three steps.
+    Chunks start inside pages (tok_start) and one has k = 0."""
+    keys_ready = mode == "keys_ready"
+    layers, pf, bt, chunks, k_new, v_new = setup_case(dev, layout, chunk_tokens=(100, 64, 37, 300), seed=4)
+    chunks = [c + (0,) for c in chunks]
+    chunks[1] = (chunks[1][0], chunks[1][1], 50, chunks[1][3], 14)      # starts at token 14 of its pages
+    chunks[2] = chunks[2][:3] + (0, 3)                                    # nothing selected
+    cpu = [t for t, _ in layers]
+    gpu = [to_dev(t, dev) for t in cpu]
+    btd = torch.from_numpy(bt).to(dev)
+    kmax = max(c[3] for c in chunks) + 2
+    if layout == "mla":
+        v_new = None
+    keys_o, sel_o = _oracle_selection(cpu, pf, bt, k_new, v_new, chunks, kmax)
+    keys = None
+    if keys_ready:
+        keys = cache_ops.kv_deviation(gpu, pf, btd, k_new.to(dev), chunks)
+    keys_g, sel_g = cache_ops.select_merge(gpu, pf, btd, k_new.to(dev), None if v_new is None else v_new.to(dev),
+                                           chunks, kmax=kmax, keys=keys, keys_ready=keys_ready,
+                                           one_pass=mode == "one_pass")
+    torch.cuda.synchronize()
+    assert np.array_equal(keys_g.cpu().numpy().view(np.uint32), keys_o.view(np.uint32))
+    assert np.array_equal(sel_g.cpu().numpy(), sel_o)
+    for t, td in zip(cpu, gpu):
+        assert same_bytes(td, t)
+
+
+@pytest.mark.parametrize("row_dtype,one_pass", [(torch.bfloat16, False), (torch.float16, False),
+                                                (torch.bfloat16, True)])
+def test_select_merge_fp8_cache(dev, row_dtype, one_pass):
+    """fp8 (e4m3) cache: keys from cached K dequantised with the per-head K
+    scales, rows quantised with the same K scales and the V scales."""
+    layers, pf, bt, chunks, _k, _v = setup_case(dev, "nhd", dtype=torch.uint8, chunk_tokens=(100, 64, 37), L=2)
+    cpu = [t for t, _ in layers]
+    gpu = [to_dev(t, dev) for t in cpu]
+    L, H, D = 2, 4, 64
+    T = chunks[-1][1] + chunks[-1][2]
+    g = torch.Generator().manual_seed(23)
+    ks = (0.01 + 0.03 * torch.rand(L, H, generator=g)).float()
+    vs = (0.01 + 0.03 * torch.rand(L, H, generator=g)).float()
+    k_new = torch.randn(L, T, H, D, generator=g).to(row_dtype)
+    v_new = torch.randn(L, T, H, D, generator=g).to(row_dtype)
+    kmax = max(c[3] for c in chunks)
+    keys_o, sel_o = _oracle_selection(cpu, pf, bt, k_new, v_new, chunks, kmax, ks.numpy(), vs.numpy())
+    keys_g, sel_g = cache_ops.select_merge(gpu, pf, torch.from_numpy(bt).to(dev), k_new.to(dev), v_new.to(dev),
+                                           chunks, k_scales=ks.to(dev), v_scales=vs.to(dev), one_pass=one_pass)
+    torch.cuda.synchronize()
+    assert np.array_equal(keys_g.cpu().numpy().view(np.uint32), keys_o.view(np.uint32))
+    assert np.array_equal(sel_g.cpu().numpy(), sel_o)
+    for t, td in zip(cpu, gpu):
+        assert same_bytes(td, t)
+
+
+def test_select_merge_long_chunk_takes_three_launches(dev):
+    """A 9000-token chunk (past the 8192 keys the fused kernel holds in LDS)
+    beside a short one: the call runs deviation, top-k and merge in turn, with
+    the same results."""
+    layers, pf, bt, chunks, k_new, v_new = setup_case(dev, "nhd", nb=600, h=2, d=64, L=1,
+                                                      chunk_tokens=(9000, 120), seed=9)
+    cpu = [t for t, _ in layers]
+    gpu = [to_dev(t, dev) for t in cpu]
+    kmax = max(c[3] for c in chunks)
+    keys_o, sel_o = _oracle_selection(cpu, pf, bt, k_new, v_new, chunks, kmax)
+    keys_g, sel_g = cache_ops.select_merge(gpu, pf, torch.from_numpy(bt).to(dev), k_new.to(dev), v_new.to(dev),
+                                           chunks)
+    torch.cuda.synchronize()
+    assert np.array_equal(keys_g.cpu().numpy().view(np.uint32), keys_o.view(np.uint32))
+    assert np.array_equal(sel_g.cpu().numpy(), sel_o)
+    assert same_bytes(gpu[0], cpu[0])
+
+
+@pytest.mark.parametrize("one_pass", [False, True])
+def test_select_merge_many_selected_rows(dev, one_pass):
+    """Chunks whose selected rows take more merge rounds than a fused
+    workgroup handles well (Llama-3-8B rows, k = 154 of 1024): the call runs
+    the three kernels, unless one_pass asks for the fused launch; results
+    bit-exact either way."""
+    layers, pf, bt, chunks, k_new, v_new = setup_case(dev, "nhd", nb=200, h=8, d=128, L=2,
+                                                      chunk_tokens=(1024, 700), seed=5)
+    cpu = [t for t, _ in layers]
+    gpu = [to_dev(t, dev) for t in cpu]
+    kmax = max(c[3] for c in chunks)
+    keys_o, sel_o = _oracle_selection(cpu, pf, bt, k_new, v_new, chunks, kmax)
+    keys_g, sel_g = cache_ops.select_merge(gpu, pf, torch.from_numpy(bt).to(dev), k_new.to(dev), v_new.to(dev),
+                                           chunks, one_pass=one_pass)
+    torch.cuda.synchronize()
+    assert np.array_equal(keys_g.cpu().numpy().view(np.uint32), keys_o.view(np.uint32))
+    assert np.array_equal(sel_g.cpu().numpy(), sel_o)
+    for t, td in zip(cpu, gpu):
+        assert same_bytes(td, t)
