@@ -167,3 +167,52 @@ def test_fused_and_selection_replays_match_eager(dev):
         assert torch.equal(cap["sel"], eager["sel"]), f"replay {rep} sel"
         _ = float(torch.randn(4096, device=dev).abs().sum())
         torch.cuda.synchronize()
+
+
+def test_select_merge_replays_match_eager(dev):
+    """select_merge (the deviation kernel, then the fused top-k and merge) of
+    three chunks, one starting inside a page, captured in a graph: every
+    replay equals the same call run eagerly."""
+    g = torch.Generator().manual_seed(5)
+    L, NB, PS, H, D = 2, 32, 16, 8, 128
+    base = [torch.randn(2, NB, PS, H, D, generator=g).to(torch.bfloat16) for _ in range(L)]
+    T = 96
+    k_new = torch.randn(L, T, H, D, generator=g).to(torch.bfloat16).to(dev)
+    v_new = torch.randn(L, T, H, D, generator=g).to(torch.bfloat16).to(dev)
+    bt = torch.tensor([4, 9, 2, 17, 23, 6], dtype=torch.int32, device=dev)
+    chunks = [(0, 0, 32, 5, 0), (2, 32, 30, 7, 2), (4, 62, 32, 0, 0)]
+
+    def make():
+        return dict(layers=[t.to(dev) for t in base],
+                    keys=torch.zeros(L, T, dtype=torch.float32, device=dev),
+                    sel=torch.zeros(L, 3, 7, dtype=torch.int32, device=dev))
+
+    def run(s):
+        cache_ops.select_merge(s["layers"], False, bt, k_new, v_new, chunks, kmax=7, keys=s["keys"],
+                               sel_idx=s["sel"])
+
+    eager, cap = make(), make()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):       # warm-up outside the capture
+        run(make())
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(cap)
+    torch.cuda.synchronize()
+    for t, b in zip(cap["layers"], base):      # capturing ran nothing
+        assert torch.equal(t.cpu().view(torch.int16), b.view(torch.int16))
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        run(eager)
+        torch.cuda.synchronize()
+        for li in range(L):
+            assert torch.equal(cap["layers"][li].view(torch.int16), eager["layers"][li].view(torch.int16)), \
+                f"replay {rep} layer {li}"
+        assert torch.equal(cap["keys"].view(torch.int32), eager["keys"].view(torch.int32)), f"replay {rep} keys"
+        assert torch.equal(cap["sel"], eager["sel"]), f"replay {rep} sel"
+        _ = float(torch.randn(4096, device=dev).abs().sum())
+        torch.cuda.synchronize()
