@@ -256,13 +256,14 @@ def test_gather_scatter_fuzz(dev, data):
         assert same_bytes(td, t)
 
 
-@FUZZ
-@given(data=st.data())
-def test_selection_fuzz(dev, data):
+def _selection_case(data, dtype=None):
+    """A drawn selection workload: layers of a drawn layout, chunks over a
+    block table with null, out-of-range and negative ids, chunk starts inside
+    their first page (tok_start) and k from 0 to past the chunk's length."""
     from oracle import select as osel
     layout = data.draw(st.sampled_from(LAYOUTS), label="layout")
-    dtype = data.draw(st.sampled_from(DTYPES), label="cache dtype")
-    new_dtype = data.draw(st.sampled_from([torch.bfloat16, torch.float16]), label="k_new dtype")
+    if dtype is None:
+        dtype = data.draw(st.sampled_from(DTYPES), label="cache dtype")
     ps = data.draw(st.sampled_from([1, 8, 16]), label="page_size")
     h = data.draw(st.sampled_from([1, 2, 4, 8]), label="heads")
     d = data.draw(st.sampled_from([8, 16, 24, 64, 128]), label="head_dim")
@@ -291,18 +292,29 @@ def test_selection_fuzz(dev, data):
                 k_used += 1
             else:
                 ids.append(nb + 2)
-        n = data.draw(st.integers(0, npg * kps), label="n_tokens")
+        ts = data.draw(st.integers(0, kps - 1), label="tok_start")
+        n = data.draw(st.integers(0, npg * kps - ts), label="n_tokens")
         k = data.draw(st.integers(0, n + 2), label="k")
-        chunks.append((len(bt), row, n, k))
+        chunks.append((len(bt), row, n, k, ts))
         bt.extend(ids)
         row += n
     T = max(row, 1)
-    bt = np.asarray(bt, np.int32)
+    return dict(layers=[t for t, _ in layers], pf=pf, bt=np.asarray(bt, np.int32), chunks=chunks, T=T, L=L,
+                H=H, D=D, dtype=dtype, g=g)
+
+
+@FUZZ
+@given(data=st.data())
+def test_selection_fuzz(dev, data):
+    from oracle import select as osel
+    c = _selection_case(data)
+    cpu, pf, bt, chunks, T, L, H, D, dtype, g = (c[k] for k in ("layers", "pf", "bt", "chunks", "T", "L", "H",
+                                                                "D", "dtype", "g"))
+    new_dtype = data.draw(st.sampled_from([torch.bfloat16, torch.float16]), label="k_new dtype")
     k_new = torch.randn(L, T, H, D, generator=g).to(new_dtype)
     scales = None
     if dtype == torch.uint8:
         scales = (0.25 + torch.rand(L, H, generator=g)).float()
-    cpu = [t for t, _ in layers]
     gpu = [to_dev(t, dev) for t in cpu]
     btd = torch.from_numpy(bt).to(dev)
     keys_o = osel.deviation(cpu, pf, bt, k_new, chunks, None if scales is None else scales.numpy())
@@ -312,7 +324,7 @@ def test_selection_fuzz(dev, data):
     kg = keys_g.cpu().numpy()
     assert np.array_equal(kg.view(np.uint32), keys_o.view(np.uint32)), \
         f"{int((kg.view(np.uint32) != keys_o.view(np.uint32)).sum())} keys differ"
-    kmax = max(min(c[3], c[2]) for c in chunks) + data.draw(st.integers(0, 3), label="kmax extra")
+    kmax = max(min(ch[3], ch[2]) for ch in chunks) + data.draw(st.integers(0, 3), label="kmax extra")
     sel_o = osel.topk_per_chunk(keys_o, chunks, kmax)
     sel_g = cache_ops.topk_per_chunk(keys_g, chunks, kmax=kmax)
     torch.cuda.synchronize()
@@ -347,6 +359,53 @@ def test_selection_fuzz(dev, data):
     cache_ops.merge_rows(gpu, pf, btd, km.to(dev), vm.to(dev), chunks, torch.from_numpy(sel_o).to(dev),
                          k_scales=None if ks is None else ks.to(dev), v_scales=None if vs is None else vs.to(dev))
     torch.cuda.synchronize()
+    for t, td in zip(cpu, gpu):
+        assert same_bytes(td, t)
+
+
+@FUZZ
+@given(data=st.data())
+def test_select_merge_fuzz(dev, data):
+    """The whole selection in one call (select_merge: default, keys given, or
+    one pass) on the drawn workloads: keys, indices and merged bytes
+    bit-exact against the oracle's three steps. fp8 caches merge bf16/fp16
+    rows quantised with the cache's K and V scales, which also dequantise
+    the cached K for the keys."""
+    from oracle import select as osel
+    c = _selection_case(data)
+    cpu, pf, bt, chunks, T, L, H, D, dtype, g = (c[k] for k in ("layers", "pf", "bt", "chunks", "T", "L", "H",
+                                                                "D", "dtype", "g"))
+    quant = dtype == torch.uint8
+    row_dtype = data.draw(st.sampled_from([torch.bfloat16, torch.float16]), label="row dtype") if quant else dtype
+    km = (torch.randn(L, T, H, D, generator=g) * (4 if quant else 1)).to(row_dtype)
+    vm = (torch.randn(L, T, H, D, generator=g) * (4 if quant else 1)).to(row_dtype)
+    ks = vs = None
+    if quant:
+        ks = (0.002 + 0.02 * torch.rand(L, H, generator=g)).float()
+        vs = (0.002 + 0.02 * torch.rand(L, H, generator=g)).float()
+    mode = data.draw(st.sampled_from(["default", "keys_ready", "one_pass"]), label="mode")
+    kmax = max(min(ch[3], ch[2]) for ch in chunks) + data.draw(st.integers(0, 3), label="kmax extra")
+    has_v = osel.v_view(cpu[0], pf) is not None
+    keys_o = osel.deviation(cpu, pf, bt, km, chunks, None if ks is None else ks.numpy())
+    sel_o = osel.topk_per_chunk(keys_o, chunks, kmax)
+    gpu = [to_dev(t, dev) for t in cpu]
+    btd = torch.from_numpy(bt).to(dev)
+    keys = None
+    if mode == "keys_ready":
+        keys = cache_ops.kv_deviation(gpu, pf, btd, km.to(dev), chunks, k_scales=None if ks is None else ks.to(dev))
+    if kmax == 0:
+        return      # no index rows: select_merge only computes the keys (checked by the selection fuzz)
+    osel.merge_rows(cpu, pf, bt, km, vm, chunks, sel_o,
+                    k_scales=None if ks is None else ks.numpy(), v_scales=None if vs is None else vs.numpy())
+    keys_g, sel_g = cache_ops.select_merge(gpu, pf, btd, km.to(dev), vm.to(dev) if has_v else None, chunks,
+                                           kmax=kmax, keys=keys, keys_ready=mode == "keys_ready",
+                                           one_pass=mode == "one_pass",
+                                           k_scales=None if ks is None else ks.to(dev),
+                                           v_scales=None if vs is None else vs.to(dev))
+    torch.cuda.synchronize()
+    kg = keys_g.cpu().numpy()
+    assert np.array_equal(kg.view(np.uint32), keys_o.view(np.uint32))
+    assert np.array_equal(sel_g.cpu().numpy(), sel_o)
     for t, td in zip(cpu, gpu):
         assert same_bytes(td, t)
 
