@@ -523,7 +523,7 @@ __global__ __launch_bounds__(kThreads) void select_merge_kernel(
     const float* __restrict__ dev_scales, float* __restrict__ keys, int32_t* __restrict__ sel, int kmax,
     int n_max, int units, FastDiv d_tok_units, FastDiv d_upr, const float* __restrict__ k_scales,
     const float* __restrict__ v_scales, int c0, int l0) {
-    extern __shared__ uint32_t s_dyn[];
+    extern __shared__ __align__(16) uint32_t s_dyn[];   // keys, indices, then 8-byte offsets
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_digit, s_above;
     __shared__ int s_wave[kWaves];

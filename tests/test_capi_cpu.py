@@ -463,3 +463,33 @@ def test_chunk_start_inside_a_page_is_checked_against_the_block_table(lib):
     assert "reads past the end of block_table" in run(1, 40, 9)        # pages 1.. + (9 + 39) // 16 = 4
     assert "negative chunk field" in run(0, 4, -1)
     assert "reads past the end" not in (run(0, 48, 16) or "")           # tokens 16..63: pages 1-3
+
+
+def test_select_merge_validation(lib):
+    """daric_select_merge refuses bad arguments before any device call (fake
+    device pointers; every case fails in validation)."""
+    bf = (_lib.DaricTensor * 1)(fake((2, 8, 16, 4, 64), torch.bfloat16))
+    f8 = (_lib.DaricTensor * 1)(fake((2, 8, 16, 4, 64), torch.uint8))
+    bt = fake((8,), torch.int32, ptr=0x20000000)
+    rows = fake((1, 64, 4, 64), torch.bfloat16, ptr=0x60000000)
+    keys = fake((1, 64), torch.float32, ptr=0x70000000)
+    sel = fake((1, 1, 4), torch.int32, ptr=0x50000000)
+    sc = fake((1, 4), torch.float32, ptr=0x80000000)
+    ch = (_lib.DaricChunk * 1)(_lib.DaricChunk(0, 0, 64, 4, 0))
+
+    def run(layers, k_sc=None, v_sc=None, flags=0, sel_t=sel, chunk=ch):
+        st = lib.daric_select_merge(layers, 1, 0, ctypes.byref(bt), ctypes.byref(rows), ctypes.byref(rows),
+                                    chunk, 1, ctypes.byref(k_sc) if k_sc is not None else None,
+                                    ctypes.byref(v_sc) if v_sc is not None else None, ctypes.byref(keys),
+                                    ctypes.byref(sel_t), flags, ctypes.c_uint64(0))
+        assert st != 0
+        return st, lib.daric_last_error().decode()
+
+    assert "unknown select_merge flags 4" in run(bf, flags=4)[1]
+    assert "apply only to an fp8 cache" in run(bf, k_sc=sc, v_sc=sc)[1]
+    assert "needs k_scales" in run(f8)[1]
+    assert "needs v_scales" in run(f8, k_sc=sc)[1]
+    small = fake((1, 1, 3), torch.int32, ptr=0x50000000)
+    assert "smaller than a chunk's k" in run(bf, sel_t=small)[1]
+    past = (_lib.DaricChunk * 1)(_lib.DaricChunk(6, 0, 40, 4, 5))   # tokens 5..44 from page 6: page 8
+    assert "reads past the end of block_table" in run(bf, chunk=past)[1]
