@@ -80,24 +80,35 @@ class CacheTopo:
         raise ValueError(f"Layer {layer_name} not found in any group.")
 
 
+def _block_ids(blocks) -> np.ndarray:
+    """A block list (list, tuple, array or tensor of ids) as int32 numpy."""
+    if isinstance(blocks, torch.Tensor):
+        return blocks.detach().to("cpu", torch.int32).reshape(-1).numpy()
+    return np.asarray(blocks, dtype=np.int32).reshape(-1)
+
+
+def _concat(parts) -> np.ndarray:
+    return np.concatenate(parts) if parts else np.zeros(0, dtype=np.int32)
+
+
 def plan_load_segments(metas, group_idx: int):
     """apply_rerotate_load's planning (adapter.py:208-265): metas with a
     non-empty chunk whose saved position differs from ptr[0] move every token
     by ptr[0] - saved_pos. Returns (block table int32, segments)."""
-    bt: list = []
+    parts: list = []
     segs = []
+    off = 0
     for meta in metas:
         old_pos = int(meta.saved_pos)
         new_pos = int(meta.ptr[0])
         n = int(meta.ptr[1] - meta.ptr[0])
         if n <= 0 or old_pos == new_pos:
             continue
-        blocks = meta.block_ids[group_idx]
-        if isinstance(blocks, torch.Tensor):
-            blocks = blocks.tolist()
-        segs.append((len(bt), 0, n, new_pos - old_pos))
-        bt.extend(int(b) for b in blocks)
-    return np.asarray(bt, dtype=np.int32), segs
+        blocks = _block_ids(meta.block_ids[group_idx])
+        segs.append((off, 0, n, new_pos - old_pos))
+        parts.append(blocks)
+        off += blocks.size
+    return _concat(parts), segs
 
 
 def plan_multi_segments(group_ptrs, block_ids_list, group_idx: int):
@@ -105,8 +116,9 @@ def plan_multi_segments(group_ptrs, block_ids_list, group_idx: int):
     more than two groups, groups 1..n-2 of non-zero length move by
     group_ptr[i] - group_ptr[0]; token offsets count from group_ptr[0] in the
     request's block list."""
-    bt: list = []
+    parts: list = []
     segs = []
+    off = 0
     for req_idx, group_ptr in enumerate(group_ptrs):
         n_groups = len(group_ptr) - 1
         if n_groups <= 2:
@@ -119,13 +131,11 @@ def plan_multi_segments(group_ptrs, block_ids_list, group_idx: int):
                 req_segs.append((group_ptr[i] - base, glen, group_ptr[i] - base))
         if not req_segs:
             continue
-        blocks = block_ids_list[req_idx][group_idx]
-        if isinstance(blocks, torch.Tensor):
-            blocks = blocks.tolist()
-        off = len(bt)
+        blocks = _block_ids(block_ids_list[req_idx][group_idx])
         segs.extend((off, t0, n, d) for t0, n, d in req_segs)
-        bt.extend(int(b) for b in blocks)
-    return np.asarray(bt, dtype=np.int32), segs
+        parts.append(blocks)
+        off += blocks.size
+    return _concat(parts), segs
 
 
 def _table_positions(max_pos: int) -> list:
@@ -265,6 +275,9 @@ class Adapter:
         self.kvcaches: dict = {}
         self.rotary_embeds: dict = {}
         self._inv_cache: dict = {}
+        self._layers: dict = {}
+        self._groups: dict = {}
+        self._bt_cache: dict = {}
         if config.recompute_policy == "daric":
             self.recompute_policy = DARICPolicy(config.recompute_avg_num, function=config.function,
                                                 r=config.r)
@@ -280,6 +293,7 @@ class Adapter:
     # ------------------------------------------------------------ registration
     def register_kvcaches(self, kvcaches: dict) -> None:
         self.kvcaches = kvcaches
+        self._layers.clear()
 
     def register_rotary_embed(self, layer_name: str, rotary_embed) -> None:
         if layer_name not in self.rotary_embeds:
@@ -307,6 +321,43 @@ class Adapter:
             dev = hit[2][str(device)] = hit[1].to(device).contiguous()
         return dev
 
+    def _group_idx(self, name: str, topo) -> int:
+        hit = self._groups.get(name)
+        if hit is None or hit[0] is not topo:
+            hit = self._groups[name] = (topo, topo.get_group_idx(name))
+        return hit[1]
+
+    def _layer_info(self, name: str, topo):
+        """(batch key, rotary, page_first) of a layer: its layout checked with
+        the reference's errors and its rotary table proven, once per (cache
+        tensor, rotary module, page_first); a per-layer call (the worker's
+        layer-wise load, worker.py:230-231) then costs a few dictionary
+        lookups instead of the checks."""
+        kv = self.kvcaches[name]
+        rotary = self.rotary_embeds[name]
+        page_first = bool(topo.layers[name].page_first)
+        hit = self._layers.get(name)
+        if hit is not None and hit[0] is kv and hit[1] is rotary and hit[2] == page_first:
+            return hit[3]
+        check_rerotate_layout(name, kv, page_first, int(rotary.rotary_dim))
+        self._host_inv_freq(rotary)     # a table the kernels cannot reproduce raises here
+        key = (tuple(kv.shape), kv.stride(), kv.dtype, page_first, id(rotary),
+               int(rotary.rotary_dim), bool(rotary.is_neox_style))
+        info = (key, rotary, page_first)
+        self._layers[name] = (kv, rotary, page_first, info)
+        return info
+
+    def _device_block_table(self, group_idx: int, bt: np.ndarray, device) -> torch.Tensor:
+        """The block table on the device. The worker's layer-wise load plans
+        the same metas for every layer, so the last table of each group is
+        kept and reused while the planned ids are equal (no copy per layer)."""
+        last = self._bt_cache.get(group_idx)
+        if last is not None and last[0] == device and np.array_equal(last[1], bt):
+            return last[2]
+        bt_dev = torch.from_numpy(bt).to(device, non_blocking=True)
+        self._bt_cache[group_idx] = (device, bt, bt_dev)
+        return bt_dev
+
     def _rotate(self, layer_names: Sequence[str], plan) -> None:
         """Runs `plan(group_idx) -> (block table, segments)` for every KV-cache
         group and rotates the group's layers, batching the layers that share a
@@ -315,7 +366,7 @@ class Adapter:
         by_group: dict = {}
         for name in layer_names:
             if name in self.kvcaches:
-                by_group.setdefault(topo.get_group_idx(name), []).append(name)
+                by_group.setdefault(self._group_idx(name, topo), []).append(name)
         work = []
         for group_idx, names in by_group.items():
             bt, segs = plan(group_idx)
@@ -326,18 +377,12 @@ class Adapter:
                 raise ValueError(f"Unsupported KV cache rank for rerotate: {kv0.ndim}")
             batches: dict = {}
             for name in names:
-                kv = self.kvcaches[name]
-                rotary = self.rotary_embeds[name]
-                page_first = bool(topo.layers[name].page_first)
-                check_rerotate_layout(name, kv, page_first, int(rotary.rotary_dim))
-                self._host_inv_freq(rotary)     # a table the kernels cannot reproduce raises here
-                key = (tuple(kv.shape), kv.stride(), kv.dtype, page_first, id(rotary),
-                       int(rotary.rotary_dim), bool(rotary.is_neox_style))
-                batches.setdefault(key, (rotary, page_first, []))[2].append(kv)
-            work.append((kv0.device, bt, segs, batches))
+                key, rotary, page_first = self._layer_info(name, topo)
+                batches.setdefault(key, (rotary, page_first, []))[2].append(self.kvcaches[name])
+            work.append((group_idx, kv0.device, bt, segs, batches))
         # every layout is checked before any layer is rotated
-        for device, bt, segs, batches in work:
-            bt_dev = torch.from_numpy(bt).to(device, non_blocking=True)
+        for group_idx, device, bt, segs, batches in work:
+            bt_dev = self._device_block_table(group_idx, bt, device)
             for rotary, page_first, kvs in batches.values():
                 cache_ops.rerotate_pages(kvs, page_first, bt_dev, segs,
                                          self._device_inv_freq(rotary, device),
