@@ -40,7 +40,7 @@ from . import cache_ops
 from .policy import DARICPolicy, plan_selection
 
 __all__ = ["AdaptionConfig", "LayerCacheTopo", "CacheTopo", "Adapter", "plan_load_segments",
-           "plan_multi_segments", "check_rerotate_layout"]
+           "plan_multi_segments", "check_rerotate_layout", "rotary_inv_freq"]
 
 
 @dataclass
@@ -223,6 +223,14 @@ def _inv_freq(rotary) -> torch.Tensor:
         f"{name}: rotary cos_sin_cache is not cos/sin(p * inv_freq) for any inverse frequencies the "
         f"module exposes (tried: {', '.join(tried) or 'none'}); re-rotation supports tables of that form "
         f"only (default, llama3- and YaRN-scaled frequencies)")
+
+
+def rotary_inv_freq(rotary) -> torch.Tensor:
+    """The fp32 inverse frequencies of a rotary module, proven against its own
+    cos_sin_cache (ValueError when none reproduces it): what a caller of the
+    fused load (scatter_pages_rerotate, KVIOContext.load(rerotate=...))
+    passes as inv_freq, so that it rotates as the Adapter does."""
+    return _inv_freq(rotary)
 
 
 def check_rerotate_layout(layer_name: str, kv: torch.Tensor, page_first: bool, rotary_dim: int) -> None:

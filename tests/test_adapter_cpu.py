@@ -170,3 +170,10 @@ def test_rotation_refused_before_any_layer_moves(monkeypatch):
     with pytest.raises(ValueError, match="OtherBaseRotary"):
         a.apply_rerotate_load(metas)
     assert rec.calls == []
+
+
+def test_rotary_inv_freq_is_the_checked_vector():
+    r = afakes.MScaleRotary(64, max_pos=4096)
+    assert torch.equal(ad.rotary_inv_freq(r), ad._inv_freq(r))
+    with pytest.raises(ValueError, match="OtherBaseRotary"):
+        ad.rotary_inv_freq(afakes.OtherBaseRotary(64, max_pos=4096))
