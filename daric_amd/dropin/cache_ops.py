@@ -12,6 +12,7 @@ from daric_amd.cache_ops import (  # noqa: F401
     kv_deviation,
     merge_rows,
     rerotate_pages,
+    select_merge,
     timing_enable,
     timing_read,
     topk_per_chunk,
