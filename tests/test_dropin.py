@@ -71,7 +71,7 @@ def test_dropin_modules_reexport_the_implementation():
     from daric_amd.dropin import adapter as dad
     from daric_amd.dropin import cache_ops as dco
     for name in ("CacheCopier", "batched_memcpy_d2h", "batched_memcpy_h2d", "rerotate_pages",
-                 "kv_deviation", "topk_per_chunk", "merge_rows"):
+                 "kv_deviation", "topk_per_chunk", "merge_rows", "select_merge"):
         assert getattr(dco, name) is getattr(cache_ops, name)
     assert dad.Adapter is ad.Adapter
 
