@@ -182,3 +182,41 @@ def test_quantising_merge_is_pinned():
                 for s in range(ps):
                     if (b, s) not in touched:
                         assert all(int(t[:, b, s].abs().sum()) == 0 for t in layer)
+
+
+def test_chunk_slots_with_a_start_inside_a_page():
+    """Token j of a chunk starting at token ts of its block list lives in page
+    bt[bo + (ts + j) // PS] at place (ts + j) % PS: against a token-by-token
+    walk over the pages."""
+    bt = np.array([7, 3, 9, 4, 11, 2], np.int32)
+    for ps in (1, 4, 16):
+        for bo, ts, n in ((0, 0, 5), (1, 3, 9), (2, ps - 1, 2 * ps), (0, 2 * ps + 1, ps)):
+            if bo + (ts + n - 1) // ps >= bt.size:
+                continue
+            walk = []
+            page, place = bo, 0
+            for _ in range(ts):                 # skip ts tokens
+                place += 1
+                if place == ps:
+                    page, place = page + 1, 0
+            for _ in range(n):
+                walk.append((int(bt[page]), place))
+                place += 1
+                if place == ps:
+                    page, place = page + 1, 0
+            blk, s = select.chunk_slots(bt, bo, n, ps, ts)
+            assert list(zip(blk.tolist(), s.tolist())) == walk
+
+
+def test_four_and_five_field_chunks_agree():
+    """A chunk given without tok_start is the chunk with tok_start 0."""
+    g = torch.Generator().manual_seed(3)
+    layer = torch.randn(2, 12, 16, 2, 16, generator=g).to(torch.bfloat16)
+    bt = np.array([5, 2, 9, 1], np.int32)
+    k_new = torch.randn(1, 40, 2, 16, generator=g).to(torch.bfloat16)
+    k4 = select.deviation([layer], False, bt, k_new, [(0, 0, 20, 3), (2, 20, 20, 4)])
+    k5 = select.deviation([layer], False, bt, k_new, [(0, 0, 20, 3, 0), (2, 20, 20, 4, 0)])
+    assert np.array_equal(k4.view(np.uint32), k5.view(np.uint32))
+    shifted = select.deviation([layer], False, bt, k_new, [(0, 0, 20, 3, 16)])   # starts on page 1
+    same = select.deviation([layer], False, bt, k_new, [(1, 0, 20, 3, 0)])
+    assert np.array_equal(shifted.view(np.uint32), same.view(np.uint32))
