@@ -177,3 +177,87 @@ def test_noalloc_calls_on_two_streams_are_ordered(dev):
         for l in range(len(dims)):
             assert same_bytes(pair[1][1][l], pair[0][1][l]), f"call {k} layer {l}"
         assert not same_bytes(pair[0][1][0], base[0])
+
+
+def test_noalloc_call_captured_in_a_graph_replays_exactly(dev):
+    """A fused call whose 48 jobs (3840 descriptor bytes) are too many for the
+    kernel arguments, which the regular entry point would stage in its
+    descriptor ring and so refuse under capture, recorded in a HIP graph
+    through the allocation-free entry point. Each replay restages its own
+    descriptors: between replays an eager call with another job list
+    overwrites the scratch array, the target layers are cleared, and every
+    replay still writes what the regular entry point writes eagerly. Neither
+    the capture nor the replays touch the descriptor ring."""
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(23)
+    rng = np.random.default_rng(23)
+    dims = [128] * 4
+    span_of = lambda l: PS * H * dims[l] * 2
+    inv = (1.0 / (500000.0 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).to(dev)
+    rope = _lib.DaricRope()
+    rope.inv_freq = inv.data_ptr()
+    rope.rotary_dim = 128
+    rope.is_neox = 1
+    perm = (rng.permutation(NB - 1) + 1).tolist()
+    # the captured call: 12 chunks x 4 layers = 48 jobs; the eager call between
+    # replays: 10 x 4 = 40 jobs on other pages of other layers
+    job_lists = [[perm[3 * i: 3 * i + 3] for i in range(12)],
+                 [perm[40 + 2 * i: 42 + 2 * i] for i in range(10)]]
+    cases = []
+    for chunks in job_lists:
+        names, offsets, sizes, flat, ioff, deltas, ntok, total = plan(len(dims), chunks, span_of, rng)
+        staging = torch.randint(-128, 127, (total,), dtype=torch.int8, generator=gen).view(torch.uint8).to(dev)
+        idx = torch.tensor(flat, dtype=torch.int32, device=dev)
+        base = make_layers(dev, dims, gen)
+        pair = []
+        for _ in range(2):
+            c = cache_ops.CacheCopier()
+            layers = [t.clone() for t in base]
+            for l, t in enumerate(layers):
+                c.register_layer(f"model.layers.{l}.self_attn.attn", t, False)
+            c.register_store(staging)
+            pair.append((c, layers))
+        cases.append((pair, (names, offsets, sizes, idx, ioff, deltas, ntok), staging))
+    for t in cases[0][0][0][1]:     # the captured call's replays start from cleared layers
+        t.zero_()
+    torch.cuda.synchronize()
+    # what each call writes, by the regular entry point, eagerly
+    for pair, args, _ in cases:
+        assert call(lib, lib.daric_copier_scatter_pages_rerotate, pair[0][0], *args, rope,
+                    torch.cuda.current_stream().cuda_stream) == 0, lib.daric_last_error()
+    torch.cuda.synchronize()
+    (cap_pair, cap_args, _), (other_pair, other_args, _) = cases
+    cap_copier, cap_layers = cap_pair[1]
+    # warm-up outside the capture (sets up the scratch array's per-GPU state)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    assert call(lib, lib.daric_copier_scatter_pages_rerotate_noalloc, cap_copier, *cap_args, rope,
+                side.cuda_stream) == 0, lib.daric_last_error()
+    torch.cuda.synchronize()
+    for t in cap_layers:
+        t.zero_()
+    torch.cuda.synchronize()
+    ring_before = counters(lib)[:2]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert call(lib, lib.daric_copier_scatter_pages_rerotate_noalloc, cap_copier, *cap_args, rope,
+                    torch.cuda.current_stream().cuda_stream) == 0, lib.daric_last_error()
+    torch.cuda.synchronize()
+    assert all(int(t.count_nonzero()) == 0 for t in cap_layers), "capturing ran the call"
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for l in range(len(dims)):
+            assert same_bytes(cap_layers[l], cap_pair[0][1][l]), f"replay {rep} layer {l}"
+        # another job list through the same scratch array, eagerly
+        other_copier, other_layers = other_pair[1]
+        assert call(lib, lib.daric_copier_scatter_pages_rerotate_noalloc, other_copier, *other_args, rope,
+                    side.cuda_stream) == 0, lib.daric_last_error()
+        torch.cuda.synchronize()
+        for l in range(len(dims)):
+            assert same_bytes(other_layers[l], other_pair[0][1][l]), f"eager call after replay {rep} layer {l}"
+        for t in cap_layers:
+            t.zero_()
+        _ = float(torch.randn(4096, device=dev).abs().sum())   # eager work between replays
+        torch.cuda.synchronize()
+    assert counters(lib)[:2] == ring_before, "the captured call or its replays used the descriptor ring"
