@@ -143,18 +143,23 @@ def test_fused_call_on_unaligned_rotary_scatters_then_rotates(dev, layout, dtype
     fused_case(dev, layout, dtype, neox, rotary_dim, seed=21)
 
 
-def inplace_case(dev, layout, dtype, neox, rotary_dim, nb=40, ps=16, h=4, d=64, L=3, seed=0):
+def inplace_case(dev, layout, dtype, neox, rotary_dim, nb=40, ps=16, h=4, d=64, L=3, seed=0, plan=None):
+    """plan(perm) -> (block table, segments), given a permutation of the
+    block ids; by default two requests' block lists with segments as
+    apply_rerotate_load/multi plan them."""
     g = torch.Generator().manual_seed(seed)
     layers = [make_layer(layout, nb, ps, h, d, dtype, g) for _ in range(L)]
     pf = layers[0][1]
     perm = np.random.default_rng(seed).permutation(np.arange(0, nb)).tolist()
-    # two requests' block lists; segments as apply_rerotate_load/multi plan them
-    metas = [(0, 40, 0, perm[0:3]), (40, 70, 0, perm[3:5]), (70, 70, 5, perm[5:6]),
-             (100, 133, 7, perm[6:9])]
-    bt, segs = orope.load_segments(metas)
-    bt2, segs2 = orope.multi_segments([[0, 10, 25, 40, 60, 64]], [perm[10:14]])
-    segs += [(o + len(bt), a, b, c) for (o, a, b, c) in segs2]
-    bt = np.concatenate([bt, bt2]).astype(np.int32)
+    if plan is not None:
+        bt, segs = plan(perm)
+    else:
+        metas = [(0, 40, 0, perm[0:3]), (40, 70, 0, perm[3:5]), (70, 70, 5, perm[5:6]),
+                 (100, 133, 7, perm[6:9])]
+        bt, segs = orope.load_segments(metas)
+        bt2, segs2 = orope.multi_segments([[0, 10, 25, 40, 60, 64]], [perm[10:14]])
+        segs += [(o + len(bt), a, b, c) for (o, a, b, c) in segs2]
+        bt = np.concatenate([bt, bt2]).astype(np.int32)
     inv = orope.default_inv_freq(rotary_dim, THETA)
     scales = None
     if dtype == torch.uint8:
@@ -177,6 +182,29 @@ def inplace_case(dev, layout, dtype, neox, rotary_dim, nb=40, ps=16, h=4, d=64, 
         mask, pn = rotation_region(t, pf, rotary_dim, slots, neox)
         worst = max(worst, assert_rotation_parity(td, t, mask, pn))
     return worst
+
+
+# Shifts of long-context models, both signs: 128K positions and past 1M. The
+# first pair's fp32 angle, shift x inv_freq[0] = shift, reaches 10^6 radians,
+# where only sincosf's argument reduction keeps cos and sin accurate.
+LONG_SHIFTS = (131071, -131072, 1048575, -1000003)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.uint8])
+def test_fused_long_context_shifts(dev, dtype):
+    fused_case(dev, "nhd", dtype, True, 128, nb=40, h=4, d=128, L=2, seed=31,
+               chunk_tokens=(37, 64, 16, 5), deltas=LONG_SHIFTS)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.uint8])
+@pytest.mark.parametrize("neox", [True, False])
+def test_inplace_long_context_shifts(dev, dtype, neox):
+    def plan(perm):
+        # (bt_offset, tok_start, n_tokens, delta); the segments' slots are distinct
+        segs = [(0, 0, 40, LONG_SHIFTS[0]), (3, 5, 20, LONG_SHIFTS[1]), (5, 0, 30, LONG_SHIFTS[2]),
+                (7, 2, 9, LONG_SHIFTS[3])]
+        return np.asarray([b for b in perm if b != 0][:8], dtype=np.int32), segs
+    inplace_case(dev, "nhd", dtype, neox, 128, nb=24, d=128, L=2, seed=33, plan=plan)
 
 
 @pytest.mark.parametrize("layout", ["nhd", "hnd", "pf", "packed", "mla"])
