@@ -207,6 +207,14 @@ def test_inplace_long_context_shifts(dev, dtype, neox):
     inplace_case(dev, "nhd", dtype, neox, 128, nb=24, d=128, L=2, seed=33, plan=plan)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.uint8])
+@pytest.mark.parametrize("neox,rotary_dim", [(True, 256), (False, 256), (True, 128)])
+def test_head_dim_256(dev, dtype, neox, rotary_dim):
+    # 256-wide heads (512-byte bf16 rows), whole and half rotary
+    fused_case(dev, "nhd", dtype, neox, rotary_dim, h=2, d=256, seed=35)
+    inplace_case(dev, "hnd", dtype, neox, rotary_dim, h=2, d=256, L=2, seed=36)
+
+
 @pytest.mark.parametrize("layout", ["nhd", "hnd", "pf", "packed", "mla"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.uint8])
 def test_inplace_layouts(dev, layout, dtype):

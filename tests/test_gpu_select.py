@@ -319,6 +319,25 @@ def test_select_merge_matches_oracle(dev, layout, mode):
         assert same_bytes(td, t)
 
 
+@pytest.mark.parametrize("layout", ["nhd", "pf"])
+def test_select_merge_head_dim_256(dev, layout):
+    """256-wide heads (two per token: 1 KiB rows): select_merge against the
+    oracle's three steps, bit-exact."""
+    layers, pf, bt, chunks, k_new, v_new = setup_case(dev, layout, h=2, d=256, chunk_tokens=(100, 64, 37),
+                                                      seed=37)
+    cpu = [t for t, _ in layers]
+    gpu = [to_dev(t, dev) for t in cpu]
+    btd = torch.from_numpy(bt).to(dev)
+    kmax = max(c[3] for c in chunks)
+    keys_o, sel_o = _oracle_selection(cpu, pf, bt, k_new, v_new, chunks, kmax)
+    keys_g, sel_g = cache_ops.select_merge(gpu, pf, btd, k_new.to(dev), v_new.to(dev), chunks, kmax=kmax)
+    torch.cuda.synchronize()
+    assert np.array_equal(keys_g.cpu().numpy().view(np.uint32), keys_o.view(np.uint32))
+    assert np.array_equal(sel_g.cpu().numpy(), sel_o)
+    for t, td in zip(cpu, gpu):
+        assert same_bytes(td, t)
+
+
 @pytest.mark.parametrize("row_dtype,one_pass", [(torch.bfloat16, False), (torch.float16, False),
                                                 (torch.bfloat16, True)])
 def test_select_merge_fp8_cache(dev, row_dtype, one_pass):
