@@ -201,3 +201,32 @@ def test_rotate_slots_cs_is_complex_multiplication(neox):
     mask = torch.ones(6 * 16, dtype=torch.bool)
     mask[slots] = False
     assert torch.equal(layer[0].reshape(96, H, D)[mask], before[0].reshape(96, H, D)[mask])
+
+
+def test_rotation_bar_needs_its_cancellation_allowance():
+    """Why the GPU rotation bar (tests.gpu_util.assert_rotation_parity) adds
+    2^-20 x the pair norm to 1 ulp. Where x1*cos - x2*sin nearly cancels, even
+    the correctly rounded bf16 result (the fp64 rotation rounded once) lies
+    more than 1 bf16 ulp from a float32 torch rotation of the same inputs:
+    float32's own rounding error, ~2^-24 x the pair norm, exceeds the bf16
+    ulp of the tiny result. With the allowance no element of the sample
+    fails, and the allowance stays 2^12 below the bf16 resolution of the
+    pair."""
+    from tests.gpu_util import ulp
+    g = torch.Generator().manual_seed(5)
+    n = 4_000_000
+    x1 = torch.randn(n, generator=g).to(torch.bfloat16).double()
+    x2 = torch.randn(n, generator=g).to(torch.bfloat16).double()
+    inv = torch.from_numpy(rope.default_inv_freq(128, 500000.0))
+    ang = (torch.randint(-8192, 8192, (n,), generator=g).float()
+           * inv[torch.randint(0, 64, (n,), generator=g)])
+    a = ang.double()
+    exact = (x1 * torch.cos(a) - x2 * torch.sin(a)).float().to(torch.bfloat16).double().numpy()
+    ref32 = (x1.float() * torch.cos(ang) - x2.float() * torch.sin(ang)).double().numpy()
+    pnorm = torch.sqrt(x1 * x1 + x2 * x2).numpy()
+    err = np.abs(exact - ref32)
+    one_ulp = ulp(np.maximum(np.abs(exact), np.abs(ref32)), torch.bfloat16)
+    literal = err > one_ulp
+    assert literal.sum() >= 1
+    assert (np.abs(ref32[literal]) < 2.0 ** -16 * pnorm[literal]).all()     # all of them cancel
+    assert (err <= one_ulp + 2.0 ** -20 * pnorm).all()
