@@ -145,7 +145,10 @@ def rotate_slots_cs(layer: torch.Tensor, page_first: bool, slots, cos, sin, rota
                     is_neox: bool) -> None:
     """Rotate in place the K rows (all heads) of slot i by its own (cos[i],
     sin[i]) rows, with the pairing and formula of _fused_rerotate_kernel
-    (adapter.py:57-88), in float64 (16-bit caches). Slots must be distinct."""
+    (adapter.py:57-88), in float64. An fp8 (uint8) cache has its e4m3 codes
+    rotated as values and re-encoded with saturating round-to-nearest-even, no
+    scale applied, as that kernel rotates a uint8 cache viewed as
+    float8_e4m3fn (adapter.py:370-373). Slots must be distinct."""
     kv = k_view(layer, page_first, rotary_dim)
     ps = kv.shape[1]
     slots = np.asarray(list(slots), dtype=np.int64)
@@ -154,7 +157,8 @@ def rotate_slots_cs(layer: torch.Tensor, page_first: bool, slots, cos, sin, rota
     assert np.unique(slots).size == slots.size
     R = int(rotary_dim)
     blk, s = torch.from_numpy(slots // ps), torch.from_numpy(slots % ps)
-    x = kv[blk, s].to(torch.float64).numpy()         # [n, H, D]
+    ones = np.ones(kv.shape[2])
+    x = _to_values(kv[blk, s], ones)                 # [n, H, D]
     c = np.asarray(cos, dtype=np.float64)[:, None, :]
     sn = np.asarray(sin, dtype=np.float64)[:, None, :]
     out = x.copy()
@@ -166,7 +170,7 @@ def rotate_slots_cs(layer: torch.Tensor, page_first: bool, slots, cos, sin, rota
         x1, x2 = x[..., 0:R:2], x[..., 1:R:2]
         out[..., 0:R:2] = x1 * c - x2 * sn
         out[..., 1:R:2] = x2 * c + x1 * sn
-    kv[blk, s] = torch.from_numpy(out.astype(np.float32)).to(layer.dtype)
+    kv[blk, s] = _from_values(out, layer.dtype, ones)
 
 
 def segment_slots(block_table, bt_offset: int, tok_start: int, n_tokens: int,

@@ -92,7 +92,9 @@ def five_metas():
 
 @pytest.mark.parametrize("layout,dtype,neox", [("nhd", torch.bfloat16, True),
                                                ("pf", torch.float16, False),
-                                               ("packed", torch.bfloat16, True)])
+                                               ("packed", torch.bfloat16, True),
+                                               ("nhd", torch.uint8, True),     # fp8 (e4m3) caches
+                                               ("pf", torch.uint8, False)])
 def test_apply_rerotate_load(dev, layout, dtype, neox):
     a, names, cpu, pf, rot = build(dev, layout, dtype, neox)
     metas = five_metas()

@@ -203,6 +203,34 @@ def test_rotate_slots_cs_is_complex_multiplication(neox):
     assert torch.equal(layer[0].reshape(96, H, D)[mask], before[0].reshape(96, H, D)[mask])
 
 
+@pytest.mark.parametrize("neox", [True, False])
+def test_rotate_slots_cs_on_fp8_codes(neox):
+    """On an e4m3 (uint8) cache the per-slot rotation rotates the code values
+    and re-encodes them: equal to torch's float8_e4m3fn cast of the complex-form
+    rotation of the decoded values (inside +-448, where that cast and
+    saturating round-to-nearest-even agree); V, the dims past R and unlisted
+    slots keep their codes."""
+    R, D, H = 32, 48, 2
+    inv = rope.default_inv_freq(R, 500000.0)
+    g = torch.Generator().manual_seed(3)
+    layer = (torch.randn(2, 6, 16, H, D, generator=g) * 4).to(torch.float8_e4m3fn).view(torch.uint8)
+    before = layer.clone()
+    slots = [3, 17, 40, 95]
+    delta = np.array([5, -9, 700, 1])
+    th = delta[:, None] * inv.astype(np.float64)[None, :]
+    rope.rotate_slots_cs(layer, False, slots, np.cos(th), np.sin(th), R, neox)
+    for i, slot in enumerate(slots):
+        b, j = slot // 16, slot % 16
+        x = before[0, b, j].view(torch.float8_e4m3fn).to(torch.float64).numpy()
+        want = rope_forward_complex(x, float(delta[i]), inv, R, neox)
+        codes = torch.from_numpy(want.astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8)
+        assert torch.equal(layer[0, b, j], codes), slot
+    assert torch.equal(layer[1], before[1])
+    mask = torch.ones(6 * 16, dtype=torch.bool)
+    mask[slots] = False
+    assert torch.equal(layer[0].reshape(96, H, D)[mask], before[0].reshape(96, H, D)[mask])
+
+
 def test_rotation_bar_needs_its_cancellation_allowance():
     """Why the GPU rotation bar (tests.gpu_util.assert_rotation_parity) adds
     2^-20 x the pair norm to 1 ulp. Where x1*cos - x2*sin nearly cancels, even
