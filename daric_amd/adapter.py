@@ -31,6 +31,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
+from itertools import chain
 from typing import List, Optional, Sequence
 
 import numpy as np
@@ -91,6 +92,18 @@ def _concat(parts) -> np.ndarray:
     return np.concatenate(parts) if parts else np.zeros(0, dtype=np.int32)
 
 
+def _id_lists(parts, total: int, plain: bool) -> np.ndarray:
+    """Block lists concatenated as int32 (`total` ids). plain: every part is a
+    list or tuple of ids, the metas' usual form, converted in one numpy call;
+    other forms are converted one by one."""
+    if plain:
+        try:
+            return np.fromiter(chain.from_iterable(parts), dtype=np.int32, count=total)
+        except (TypeError, ValueError):     # nested lists: converted one by one below
+            pass
+    return _concat([_block_ids(p) for p in parts])
+
+
 def plan_load_segments(metas, group_idx: int):
     """apply_rerotate_load's planning (adapter.py:208-265): metas with a
     non-empty chunk whose saved position differs from ptr[0] move every token
@@ -98,17 +111,21 @@ def plan_load_segments(metas, group_idx: int):
     parts: list = []
     segs = []
     off = 0
+    plain = True
     for meta in metas:
         old_pos = int(meta.saved_pos)
         new_pos = int(meta.ptr[0])
         n = int(meta.ptr[1] - meta.ptr[0])
         if n <= 0 or old_pos == new_pos:
             continue
-        blocks = _block_ids(meta.block_ids[group_idx])
+        blocks = meta.block_ids[group_idx]
+        if type(blocks) not in (list, tuple):
+            blocks = _block_ids(blocks)
+            plain = False
         segs.append((off, 0, n, new_pos - old_pos))
         parts.append(blocks)
-        off += blocks.size
-    return _concat(parts), segs
+        off += len(blocks)
+    return _id_lists(parts, off, plain), segs
 
 
 def plan_multi_segments(group_ptrs, block_ids_list, group_idx: int):
@@ -119,6 +136,7 @@ def plan_multi_segments(group_ptrs, block_ids_list, group_idx: int):
     parts: list = []
     segs = []
     off = 0
+    plain = True
     for req_idx, group_ptr in enumerate(group_ptrs):
         n_groups = len(group_ptr) - 1
         if n_groups <= 2:
@@ -131,11 +149,14 @@ def plan_multi_segments(group_ptrs, block_ids_list, group_idx: int):
                 req_segs.append((group_ptr[i] - base, glen, group_ptr[i] - base))
         if not req_segs:
             continue
-        blocks = _block_ids(block_ids_list[req_idx][group_idx])
+        blocks = block_ids_list[req_idx][group_idx]
+        if type(blocks) not in (list, tuple):
+            blocks = _block_ids(blocks)
+            plain = False
         segs.extend((off, t0, n, d) for t0, n, d in req_segs)
         parts.append(blocks)
-        off += blocks.size
-    return _concat(parts), segs
+        off += len(blocks)
+    return _id_lists(parts, off, plain), segs
 
 
 def _table_positions(max_pos: int) -> list:
@@ -360,7 +381,7 @@ class Adapter:
         the same metas for every layer, so the last table of each group is
         kept and reused while the planned ids are equal (no copy per layer)."""
         last = self._bt_cache.get(group_idx)
-        if last is not None and last[0] == device and np.array_equal(last[1], bt):
+        if last is not None and last[0] == device and last[1].tobytes() == bt.tobytes():
             return last[2]
         bt_dev = torch.from_numpy(bt).to(device, non_blocking=True)
         self._bt_cache[group_idx] = (device, bt, bt_dev)

@@ -32,6 +32,28 @@ def test_load_planning_matches_oracle():
     assert bt1.tolist() == [b + 1000 for b in obt.tolist()] and segs1 == osegs
 
 
+@pytest.mark.parametrize("form", ["list", "tuple", "numpy", "tensor", "nested", "mixed"])
+def test_planning_takes_every_block_list_form(form):
+    """Block lists as lists, tuples, numpy arrays, torch tensors, nested lists
+    or a mix plan the same block table as plain lists."""
+    lists = [[5, 9, 12], [3], [40, 41], [7, 8, 6, 2]]
+
+    def as_form(i, b):
+        f = form if form != "mixed" else ["list", "numpy", "tensor", "tuple"][i % 4]
+        return {"list": list(b), "tuple": tuple(b), "numpy": np.asarray(b, dtype=np.int64),
+                "tensor": torch.tensor(b, dtype=torch.int32), "nested": [[x] for x in b]}[f]
+
+    metas = [FakeMeta(f"c{i}", [16 * i, 16 * i + 10], 3 + i, (as_form(i, b),)) for i, b in enumerate(lists)]
+    ref = [FakeMeta(f"c{i}", [16 * i, 16 * i + 10], 3 + i, (b,)) for i, b in enumerate(lists)]
+    bt, segs = ad.plan_load_segments(metas, 0)
+    rbt, rsegs = ad.plan_load_segments(ref, 0)
+    assert bt.dtype == np.int32 and bt.tolist() == rbt.tolist() == sum(lists, []) and segs == rsegs
+    ptrs = [[0, 4, 9, 20, 30]] * len(lists)
+    bt, segs = ad.plan_multi_segments(ptrs, [(as_form(i, b),) for i, b in enumerate(lists)], 0)
+    rbt, rsegs = ad.plan_multi_segments(ptrs, [(b,) for b in lists], 0)
+    assert bt.dtype == np.int32 and bt.tolist() == rbt.tolist() and segs == rsegs
+
+
 def test_multi_planning_matches_oracle():
     ptrs = [[10, 20, 30, 45, 50], [0, 5, 9], [0, 16, 16, 40, 64, 80]]
     blocks = [([1, 2, 3, 4],), ([9],), ([5, 6, 7, 8, 11],)]
