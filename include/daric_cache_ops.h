@@ -361,14 +361,18 @@ int daric_merge_rows(const daric_tensor* layers, int64_t n_layers, int page_firs
  * dequantise the cached K for the keys and quantise the merged K rows) and
  * v_scales the V scales; k_new and v_new are bfloat16 or float16 rows. Other
  * caches take rows of their own type and NULL scales.
- * Chunks of up to 8192 tokens whose rows the merge kernel takes: the keys
- * come from the deviation kernel, then one workgroup per (layer, chunk) runs
- * the chunk's top-k on its keys in LDS and merges the selected rows, with no
- * index round trip through memory. DARIC_SELECT_ONE_PASS computes the keys
+ * Where every chunk has at most 8192 tokens, its keys and kmax row slots fit
+ * in 48 KiB of LDS, the merge kernel takes the rows, and kmax selected K and
+ * V rows make at most 12 rounds of 2048 16-byte units (e.g. 77 of 512 rows
+ * of 8 x 128 bf16, not 205 of 2048): the keys come from the deviation
+ * kernel, then one workgroup per (layer, chunk) runs the chunk's top-k on
+ * its keys in LDS and merges the selected rows, with no index round trip
+ * through memory (one workgroup walking more rounds measured slower than the
+ * merge kernel's spread). DARIC_SELECT_ONE_PASS computes the keys
  * in that workgroup too (one launch; it measured 4-7% slower on MI355X at
- * the Llama-3-8B and -70B selection workloads, and is kept for measurement).
- * Other calls run the three kernels in turn. New entry point; no counterpart
- * in the reference. */
+ * the Llama-3-8B and -70B selection workloads, and is kept for measurement;
+ * it lifts the 12-round limit). Other calls run the three kernels in turn.
+ * New entry point; no counterpart in the reference. */
 #define DARIC_SELECT_KEYS_READY 1
 #define DARIC_SELECT_ONE_PASS 2
 int daric_select_merge(const daric_tensor* layers, int64_t n_layers, int page_first,
