@@ -934,7 +934,15 @@ def main():
                "place": run_placement}
     for cname in [x.strip() for x in a.extra.split(",") if x.strip() and x.strip() != "none"]:
         key = "placement" if cname == "place" else f"config{cname}"
-        extra[key] = runners[cname](max(3, a.steps // 2), max(1, a.warmup))
+        # a secondary configuration that raises (out of memory on a shared
+        # box, say) is recorded as such; the headline line is still printed
+        try:
+            extra[key] = runners[cname](max(3, a.steps // 2), max(1, a.warmup))
+        except (RuntimeError, ValueError, MemoryError) as e:
+            extra[key] = {"error": f"{type(e).__name__}: {e}"}
+            print(f"bench: {key} failed: {e}", file=sys.stderr, flush=True)
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
     cpu = None if a.no_cpu else run_cpu_baseline(cfg, a.cpu_budget)
     line = {
         "metric": "reused KV tokens/sec (re-rotate+scatter) at Llama-3-8B shape; HBM GB/s",
