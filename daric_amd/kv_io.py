@@ -26,11 +26,15 @@ direction has a lock, where the reference lets concurrent calls share one
 staging buffer. close() drains the context as the reference's
 RankIPCContext.close does (gpu_kv_io.py:157-205).
 
-The host buffer must be page-locked memory (torch pin_memory or hipHostMalloc)
-so the DMA engines can reach it.
+The host buffer must be page-locked memory so the DMA engines can reach it:
+torch pin_memory or hipHostMalloc, or an existing buffer (the store's shared
+memory) registered with HostMemoryRegistration, as the reference registers its
+shm (gpu_kv_io.py:40-100, 236-260).
 """
 from __future__ import annotations
 
+import ctypes
+import os
 import threading
 from contextlib import contextmanager
 from typing import List, Optional, Sequence
@@ -39,9 +43,10 @@ import numpy as np
 import torch
 
 from . import cache_ops
+from .host_runtime import HOST_MEMORY_ALREADY_REGISTERED
 
-__all__ = ["POSITION_SIZE", "REGISTRATION_CHUNK_BYTES", "KVIOContext", "split_registration_copies",
-           "build_copy_plan", "per_meta_cache_size"]
+__all__ = ["POSITION_SIZE", "REGISTRATION_CHUNK_BYTES", "KVIOContext", "HostMemoryRegistration",
+           "split_registration_copies", "build_copy_plan", "per_meta_cache_size"]
 
 POSITION_SIZE = 4096
 INT64_SIZE = 8
@@ -73,6 +78,79 @@ def split_registration_copies(stg_offsets, shm_offsets, sizes, chunk_bytes=REGIS
     lo = np.maximum(host[region], (first[region] + k) * chunk_bytes)
     hi = np.minimum(host[region] + size[region], (first[region] + k + 1) * chunk_bytes)
     return (stg[region] + (lo - host[region])).tolist(), lo.tolist(), (hi - lo).tolist()
+
+
+class HostMemoryRegistration:
+    """Page-locks an existing host buffer (the store's shared-memory record
+    pool) in pieces of chunk_bytes through a host runtime
+    (host_runtime.get_gpu_host_runtime()), as the reference's
+    HostMemoryRegistration does (gpu_kv_io.py:40-100); the batched host copies
+    are then cut at the same piece boundaries (split_registration_copies).
+
+    register(buf) takes a writable buffer (e.g. SharedMemory.buf) or a CPU
+    tensor whose start and chunk_bytes are page-aligned. A piece the runtime
+    reports as already registered, or any other failure, raises RuntimeError
+    after the pieces locked so far are unlocked (pieces that cannot be
+    unlocked stay listed in `addresses`; the first error is the one raised).
+    unregister() unlocks in reverse order and raises RuntimeError if any
+    piece stays locked, keeping those in `addresses`."""
+
+    def __init__(self, runtime, chunk_bytes: int = REGISTRATION_CHUNK_BYTES):
+        self.runtime = runtime
+        self.chunk_bytes = int(chunk_bytes)
+        self.addresses: List[int] = []
+
+    @staticmethod
+    def _span(buf):
+        if isinstance(buf, torch.Tensor):
+            if buf.is_cuda or not buf.is_contiguous():
+                raise ValueError("host buffer must be a contiguous CPU tensor")
+            return buf.data_ptr(), buf.numel() * buf.element_size()
+        view = memoryview(buf)
+        if view.readonly:
+            raise ValueError("host buffer must be writable")
+        if view.nbytes == 0:
+            raise ValueError("host buffer must not be empty")
+        return ctypes.addressof(ctypes.c_char.from_buffer(view)), view.nbytes
+
+    def register(self, buf) -> None:
+        if self.addresses:
+            raise RuntimeError("host buffer is still registered; unregister() it first")
+        address, size = self._span(buf)
+        page = os.sysconf("SC_PAGE_SIZE")
+        if address % page or self.chunk_bytes <= 0 or self.chunk_bytes % page:
+            raise ValueError("host buffer start and registration chunk size must be page-aligned")
+        if size <= 0:
+            raise ValueError("host buffer must not be empty")
+        try:
+            for off in range(0, size, self.chunk_bytes):
+                status = self.runtime.register(address + off, min(self.chunk_bytes, size - off))
+                if status == HOST_MEMORY_ALREADY_REGISTERED:
+                    raise RuntimeError(f"host buffer piece at offset {off} overlaps memory that is "
+                                       "already page-locked")
+                if status != 0:
+                    raise RuntimeError(f"{self.runtime.prefix}HostRegister failed at offset {off} "
+                                       f"with status {status}")
+                self.addresses.append(address + off)
+        except BaseException:
+            try:
+                self.unregister()
+            except RuntimeError:
+                pass
+            raise
+
+    def unregister(self) -> None:
+        kept = []
+        for address in reversed(self.addresses):
+            try:
+                status = self.runtime.unregister(address)
+            except Exception:
+                status = -1
+            if status != 0:
+                kept.append(address)
+        self.addresses = kept[::-1]
+        if kept:
+            raise RuntimeError(f"{len(kept)} piece(s) of the host buffer could not be unregistered")
 
 
 def per_meta_cache_size(layer_names, group_idxs, layer_bpbs, block_ids_list, layer_name=None):
@@ -133,11 +211,15 @@ class KVIOContext:
     def __init__(self, layer_names: Sequence[str], group_idxs: Sequence[int],
                  layer_bpbs: Sequence[int], page_firsts: Sequence[bool],
                  kv_caches: dict, host: torch.Tensor, staging_bytes: int = DEFAULT_STAGING_BYTES,
-                 device: Optional[torch.device] = None):
+                 device: Optional[torch.device] = None, host_registered: bool = False):
         if host.dtype != torch.uint8 or host.dim() != 1 or host.is_cuda:
             raise ValueError("host records must be a 1-D uint8 CPU tensor")
-        if not host.is_pinned():
-            raise ValueError("host records must be page-locked (pin_memory=True)")
+        # host_registered: the caller page-locked the buffer itself
+        # (HostMemoryRegistration); torch's is_pinned() is then not consulted,
+        # as the reference's batched copies do not consult it (bindings.cpp:17-29)
+        if not host_registered and not host.is_pinned():
+            raise ValueError("host records must be page-locked (pin_memory=True, or registered with "
+                             "HostMemoryRegistration and host_registered=True)")
         self.layer_names = list(layer_names)
         self.group_idxs = list(group_idxs)
         self.layer_bpbs = list(layer_bpbs)

@@ -68,12 +68,17 @@ def test_signatures_match_reference_stub():
 
 
 def test_dropin_modules_reexport_the_implementation():
+    from daric_amd import host_runtime
     from daric_amd.dropin import adapter as dad
     from daric_amd.dropin import cache_ops as dco
+    from daric_amd.dropin import gpu_runtime as dgr
     for name in ("CacheCopier", "batched_memcpy_d2h", "batched_memcpy_h2d", "rerotate_pages",
                  "kv_deviation", "topk_per_chunk", "merge_rows", "select_merge"):
         assert getattr(dco, name) is getattr(cache_ops, name)
     assert dad.Adapter is ad.Adapter
+    # the names daric/utils/__init__.py:17 imports from gpu_runtime
+    assert dgr.get_gpu_host_runtime is host_runtime.get_gpu_host_runtime
+    assert dgr.HOST_MEMORY_ALREADY_REGISTERED == 712
 
 
 STANDIN_CONFIGS = '''
@@ -91,6 +96,7 @@ sys.path[:0] = [TREE, REPO]
 from daric import cache_ops                       # gpu_kv_io.py:9 (package-relative there)
 from daric.adaption import Adapter                # cache_engine.py:12
 from daric.configs import AdaptionConfig, CacheTopo, LayerCacheTopo, ProcessLocalConfig
+from daric.utils import get_gpu_host_runtime, HOST_MEMORY_ALREADY_REGISTERED   # gpu_kv_io.py:9-18
 import daric_amd.adapter, daric_amd.cache_ops
 names = ["model.layers.1.attn", "model.layers.0.attn", "model.layers.2.attn"]
 ProcessLocalConfig.cache_topo = CacheTopo(
@@ -103,6 +109,8 @@ print(json.dumps({
     "adapter": Adapter is daric_amd.adapter.Adapter,
     "num_layers": a.num_layers,
     "topo": a.cache_topo is ProcessLocalConfig.cache_topo,
+    "host_runtime": get_gpu_host_runtime().prefix,
+    "already_registered": HOST_MEMORY_ALREADY_REGISTERED,
 }))
 '''
 
@@ -112,8 +120,13 @@ def test_dropin_files_import_like_the_reference(tmp_path):
     pkg = tree / "daric"
     (pkg / "adaption").mkdir(parents=True)
     (pkg / "configs").mkdir()
+    (pkg / "utils").mkdir()
     (pkg / "__init__.py").write_text("")
     shutil.copy(os.path.join(DROPIN, "cache_ops.py"), pkg / "cache_ops.py")
+    shutil.copy(os.path.join(DROPIN, "gpu_runtime.py"), pkg / "utils" / "gpu_runtime.py")
+    # the reference's utils/__init__.py:17 import
+    (pkg / "utils" / "__init__.py").write_text(
+        "from .gpu_runtime import get_gpu_host_runtime, HOST_MEMORY_ALREADY_REGISTERED\n")
     shutil.copy(os.path.join(DROPIN, "adapter.py"), pkg / "adaption" / "adapter.py")
     (pkg / "adaption" / "__init__.py").write_text("from .adapter import Adapter\n")
     (pkg / "configs" / "__init__.py").write_text(STANDIN_CONFIGS)
@@ -121,7 +134,8 @@ def test_dropin_files_import_like_the_reference(tmp_path):
     r = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout.strip().splitlines()[-1])
-    assert out == {"copier": True, "memcpy": True, "adapter": True, "num_layers": 3, "topo": True}
+    assert out == {"copier": True, "memcpy": True, "adapter": True, "num_layers": 3, "topo": True,
+                   "host_runtime": "hip", "already_registered": 712}
 
 
 # ------------------------------------------------------------------ Adapter(config)
