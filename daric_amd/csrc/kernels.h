@@ -178,6 +178,10 @@ struct ScratchState;
 class ScratchUse {
 public:
     ScratchUse(int device, hipStream_t stream);
+    // A call that stops before finish() (an error after some of its kernels
+    // were enqueued) still records the event, so that later calls order
+    // after whatever it enqueued.
+    ~ScratchUse();
     ScratchUse(const ScratchUse&) = delete;
     ScratchUse& operator=(const ScratchUse&) = delete;
     uint8_t* ptr() const;
@@ -188,6 +192,7 @@ private:
     hipStream_t stream_;
     std::unique_lock<std::mutex> lock_;
     bool capture_ = false;
+    bool finished_ = false;
 };
 // Cross-stream waits ScratchUse has enqueued since the library was loaded.
 int64_t scratch_stream_waits();

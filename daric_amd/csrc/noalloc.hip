@@ -101,10 +101,21 @@ ScratchUse::ScratchUse(int device, hipStream_t stream)
 uint8_t* ScratchUse::ptr() const { return state_->ptr; }
 
 void ScratchUse::finish() {
+    finished_ = true;
     if (capture_) return;
     DARIC_HIP_CHECK(hipEventRecord(state_->done, stream_));
     state_->last = stream_;
     state_->recorded = true;
+}
+
+ScratchUse::~ScratchUse() {
+    if (finished_ || capture_) return;
+    if (hipEventRecord(state_->done, stream_) == hipSuccess) {
+        state_->last = stream_;
+        state_->recorded = true;
+    } else {
+        (void)hipGetLastError();
+    }
 }
 
 int64_t scratch_stream_waits() { return g_scratch_waits.load(std::memory_order_relaxed); }
