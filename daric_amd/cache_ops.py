@@ -7,10 +7,11 @@ functions batched_memcpy_d2h / batched_memcpy_h2d keep their signatures,
 argument meaning and errors (RuntimeError with the reference's message text).
 
 Additions (no reference counterpart; the .pyi grows, nothing changes):
-  CacheCopier.register_k_scale, CacheCopier.scatter_pages_rerotate,
+  CacheCopier.register_k_scale, CacheCopier.scatter_pages_rerotate (and its
+  allocation-free form scatter_pages_rerotate_noalloc),
   CacheCopier.gather_tokens / scatter_tokens (token-major staging for any
   cache layout), rerotate_pages, kv_deviation, topk_per_chunk, merge_rows,
-  kernel timing.
+  select_merge (the three selection calls in one), kernel timing.
 
 Every call is asynchronous on `stream` (0 = the current torch stream of the
 first layer's device, as in reference copier.cpp:27-30). The wrapper keeps
@@ -31,7 +32,8 @@ from ._lib import I64, DaricChunk, DaricRope, DaricRopeSegment, check, desc, loa
 
 __all__ = [
     "CacheCopier", "batched_memcpy_d2h", "batched_memcpy_h2d", "rerotate_pages",
-    "kv_deviation", "topk_per_chunk", "merge_rows", "timing_enable", "timing_read",
+    "kv_deviation", "topk_per_chunk", "merge_rows", "select_merge", "SELECT_KEYS_READY",
+    "SELECT_ONE_PASS", "timing_enable", "timing_read",
 ]
 
 
