@@ -549,7 +549,7 @@ def run_config4(steps, warmup, seed=0):
     blocks, bpb, rec, rec_offs = plan["blocks"], plan["bpb"], plan["rec"], plan["offsets"]
     host_rec = torch.empty(len(blocks) * rec, dtype=torch.uint8, pin_memory=True)
     io = KVIOContext(names, [0] * L, bpb, [False] * L, dict(zip(names, cache)), host_rec,
-                     staging_bytes=1 << 30)
+                     staging_bytes=512 << 20)
 
     def timed(fn):
         torch.cuda.synchronize()

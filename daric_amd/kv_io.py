@@ -11,13 +11,15 @@ position.
 
 Pipeline: the reference gathers a batch into one staging buffer, copies it to
 host, and only then gathers the next batch, with a full stream synchronisation
-per load chunk. Here each direction's staging is split into two halves: the
-copy kernels run on a kernel stream and the host DMA on a DMA stream, so batch
+per load chunk. Here each direction has two staging buffers of staging_bytes
+(the reference's one, DARIC_KV_IPC_STAGING_MB, default 256 MiB): the copy
+kernels run on a kernel stream and the host DMA on a DMA stream, so batch
 b+1's gather (scatter) overlaps batch b's device-to-host (host-to-device)
-copy; events order each half's reuse. All streams keep the default priority.
-Batching keeps the reference's limits: at most MAX_BATCH_SIZE metas and one
-staging half of bytes per batch on store; load chunks bounded by the staging
-half.
+copy; events order each buffer's reuse. All streams keep the default
+priority. Batching keeps the reference's limits: at most MAX_BATCH_SIZE metas
+and staging_bytes per batch on store, load chunks of at most staging_bytes,
+and a meta larger than staging_bytes is refused, as the reference refuses it
+(gpu_kv_io.py:445-462).
 
 Store and load have separate staging buffers and streams, as the reference's
 staging and read_staging (gpu_kv_io.py:150-151), so one thread may store while
@@ -51,7 +53,18 @@ __all__ = ["POSITION_SIZE", "REGISTRATION_CHUNK_BYTES", "KVIOContext", "HostMemo
 POSITION_SIZE = 4096
 INT64_SIZE = 8
 REGISTRATION_CHUNK_BYTES = 1 << 30
-DEFAULT_STAGING_BYTES = 256 << 20
+
+
+def _staging_bytes_from_env() -> int:
+    """The reference's staging size setting (gpu_kv_io.py:30-34):
+    DARIC_KV_IPC_STAGING_MB, default 256, must be positive."""
+    mb = int(os.environ.get("DARIC_KV_IPC_STAGING_MB", "256"))
+    if mb <= 0:
+        raise ValueError(f"DARIC_KV_IPC_STAGING_MB must be positive, got {mb}")
+    return mb << 20
+
+
+DEFAULT_STAGING_BYTES = _staging_bytes_from_env()
 
 
 def split_registration_copies(stg_offsets, shm_offsets, sizes, chunk_bytes=REGISTRATION_CHUNK_BYTES):
@@ -189,9 +202,10 @@ def build_copy_plan(layer_names, group_idxs, layer_bpbs, offsets, block_ids_list
 
 
 class _Pipe:
-    """One direction's double-buffered staging: two halves of `half` bytes, a
-    stream for the copy kernels, a stream for the host DMA, and per half the
-    event after which it may be overwritten."""
+    """One direction's double-buffered staging: two buffers ("halves") of
+    `half` bytes in one allocation, a stream for the copy kernels, a stream
+    for the host DMA, and per buffer the event after which it may be
+    overwritten."""
 
     def __init__(self, half: int, device: torch.device):
         self.half = half
@@ -204,7 +218,8 @@ class _Pipe:
 class KVIOContext:
     """One GPU's store/load context: a write copier (gathers into the store
     staging) and a read copier (scatters from the load staging), each direction
-    with two staging halves, a kernel stream and a DMA stream."""
+    with two staging buffers of staging_bytes, a kernel stream and a DMA
+    stream."""
 
     MAX_BATCH_SIZE = 4
 
@@ -227,7 +242,7 @@ class KVIOContext:
         first = kv_caches[self.layer_names[0]]
         self.device = device if device is not None else first.device
         self.host = host
-        self.half = int(staging_bytes) // 2 // 256 * 256
+        self.half = int(staging_bytes) // 256 * 256
         if self.half <= 0:
             raise ValueError("staging_bytes too small")
         self._store = _Pipe(self.half, self.device)
@@ -325,7 +340,8 @@ class KVIOContext:
                 j += 1
             if j == i:
                 raise RuntimeError(f"KV IO: single meta is {sizes[i]} bytes, larger than the "
-                                   f"{cap}-byte staging half; raise staging_bytes")
+                                   f"{cap}-byte staging buffer; raise staging_bytes "
+                                   f"(DARIC_KV_IPC_STAGING_MB)")
             yield i, j
             i = j
 

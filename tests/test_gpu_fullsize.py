@@ -251,7 +251,7 @@ def test_config4_store_load_full_size(dev):
     blocks, rec = plan["blocks"], plan["rec"]
     host = torch.empty(len(blocks) * rec, dtype=torch.uint8, pin_memory=True)
     io = KVIOContext(names, [0] * L, plan["bpb"], [False] * L, dict(zip(names, cache)), host,
-                     staging_bytes=1 << 30)
+                     staging_bytes=512 << 20)
     positions = [int(x) for x in np.random.default_rng(4).integers(-(1 << 40), 1 << 40, len(blocks))]
     io.store(plan["offsets"], blocks, positions)
     span = plan["bpb"][0] // 2
@@ -267,7 +267,7 @@ def test_config4_store_load_full_size(dev):
     del io
     cache2 = [torch.zeros_like(t) for t in cache]
     io2 = KVIOContext(names, [0] * L, plan["bpb"], [False] * L, dict(zip(names, cache2)), host,
-                      staging_bytes=1 << 30)
+                      staging_bytes=512 << 20)
     saved = io2.load(plan["offsets"], blocks)
     io2.done.synchronize()
     assert saved == positions

@@ -52,7 +52,7 @@ def record_offsets(ctx, blocks, gap=4096 + 256):
     return offs, o
 
 
-@pytest.mark.parametrize("two_groups,staging", [(False, 1 << 20), (True, 600 << 10)])
+@pytest.mark.parametrize("two_groups,staging", [(False, 512 << 10), (True, 300 << 10)])
 def test_store_then_load_matches_oracle(dev, two_groups, staging):
     names, cpu, pf, bpb, groups = setup(dev, two_groups=two_groups)
     rng = np.random.default_rng(1)
@@ -87,7 +87,7 @@ def test_layerwise_and_null_blocks(dev):
     host = torch.zeros(8 << 20, dtype=torch.uint8, pin_memory=True)
     shm = torch.zeros(8 << 20, dtype=torch.uint8)
     dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
-    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, dev_caches, host, staging_bytes=1 << 20)
+    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, dev_caches, host, staging_bytes=512 << 10)
     offs = [4096 + i * (1 << 20) for i in range(3)]
     ctx.store(offs, blocks, [5, 6, 7], layer_name=names[1])
     okv.OracleKVIO(names, groups, bpb, [pf] * 3, cpu, shm).store(offs, blocks, [5, 6, 7], layer_name=names[1])
@@ -96,7 +96,7 @@ def test_layerwise_and_null_blocks(dev):
     blocks0 = [([0] + b[0][1:],) for b in blocks]
     fresh_cpu = {n: torch.full_like(t, 7) for n, t in cpu.items()}
     fresh_dev = {n: to_dev(t, dev) for n, t in fresh_cpu.items()}
-    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, fresh_dev, host, staging_bytes=1 << 20)
+    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, fresh_dev, host, staging_bytes=512 << 10)
     assert ctx2.load(offs, blocks0, layer_name=names[1]) == [5, 6, 7]
     torch.cuda.synchronize()
     okv.OracleKVIO(names, groups, bpb, [pf] * 3, fresh_cpu, shm).load(offs, blocks0, layer_name=names[1])
@@ -119,7 +119,7 @@ def test_load_rerotate_matches_oracle(dev, two_groups, layerwise, layout):
     shm = torch.zeros(32 << 20, dtype=torch.uint8)
     dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
     L = len(names)
-    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * L, dev_caches, host, staging_bytes=640 << 10)
+    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * L, dev_caches, host, staging_bytes=320 << 10)
     offs, _ = record_offsets(ctx, blocks)
     saved = [0, 512, 77, 3000, 9]
     layer = names[2] if layerwise else None
@@ -133,7 +133,7 @@ def test_load_rerotate_matches_oracle(dev, two_groups, layerwise, layout):
     ntok = [min(len(g) for g in b) * 16 - 3 for b in blocks]
     fresh_cpu = {n: torch.zeros_like(t) for n, t in cpu.items()}
     fresh_dev = {n: to_dev(t, dev) for n, t in fresh_cpu.items()}
-    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * L, fresh_dev, host, staging_bytes=640 << 10)
+    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * L, fresh_dev, host, staging_bytes=320 << 10)
     got = ctx2.load(offs, blocks, layer_name=layer,
                     rerotate=(new_pos, ntok, torch.from_numpy(inv).to(dev), R, True))
     torch.cuda.synchronize()
@@ -166,7 +166,7 @@ def test_store_and_load_from_two_threads(dev):
     src_y, blk_x, dst_l = cut(0, 12), cut(36, 12), cut(72, 12)     # disjoint block sets
     host = torch.zeros(64 << 20, dtype=torch.uint8, pin_memory=True)
     dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
-    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, dev_caches, host, staging_bytes=320 << 10)
+    ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * 3, dev_caches, host, staging_bytes=160 << 10)
     rec = ctx.record_size(src_y[0])
     offs_y = [8192 + k * (rec + 512) for k in range(12)]
     offs_x = [(16 << 20) + k * (rec + 512) for k in range(12)]
@@ -236,7 +236,7 @@ if KV_FUZZ is not None:
         host = torch.zeros(32 << 20, dtype=torch.uint8, pin_memory=True)
         dev_caches = {n: to_dev(t, dev) for n, t in cpu.items()}
         ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * n_layers, dev_caches, host,
-                                staging_bytes=data.draw(st.sampled_from([320 << 10, 1 << 20, 8 << 20]),
+                                staging_bytes=data.draw(st.sampled_from([160 << 10, 512 << 10, 4 << 20]),
                                                         label="staging"))
         offs, o = [], 4096
         for b in blocks:
@@ -245,8 +245,8 @@ if KV_FUZZ is not None:
         saved = [int(x) for x in rng.integers(0, 1 << 40, n_meta)]
         try:
             ctx.store(offs, blocks, saved, layer_name=layer_name)
-        except RuntimeError as e:           # a meta larger than a staging half: refused up front
-            assert "staging half" in str(e)
+        except RuntimeError as e:           # a meta larger than a staging buffer: refused up front
+            assert "staging buffer" in str(e)
             return
         shm = torch.zeros(32 << 20, dtype=torch.uint8)
         okv.OracleKVIO(names, groups, bpb, [pf] * n_layers, cpu, shm).store(offs, blocks, saved,
@@ -254,7 +254,7 @@ if KV_FUZZ is not None:
         assert torch.equal(host, shm)
         fresh_cpu = {n: torch.zeros_like(t) for n, t in cpu.items()}
         fresh_dev = {n: to_dev(t, dev) for n, t in fresh_cpu.items()}
-        ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * n_layers, fresh_dev, host, staging_bytes=1 << 20)
+        ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * n_layers, fresh_dev, host, staging_bytes=512 << 10)
         # the fused re-rotating load: K of each meta's first tokens moved from
         # the saved position to a drawn one
         rerot = None
@@ -300,7 +300,7 @@ def test_concurrent_stores_take_turns_and_close_drains(dev):
     host_size = 64 << 20
     host = torch.zeros(host_size, dtype=torch.uint8, pin_memory=True)
     ctx = kv_io.KVIOContext(names, groups, bpb, [pf] * len(names), dev_caches, host,
-                            staging_bytes=512 << 10)
+                            staging_bytes=256 << 10)
     offs, end = record_offsets(ctx, blocks)
     saved = [int(x) for x in rng.integers(0, 1 << 40, len(blocks))]
     errors = []
@@ -323,7 +323,7 @@ def test_concurrent_stores_take_turns_and_close_drains(dev):
     assert torch.equal(host, shm)
     # close while a load is running in another thread
     fresh = {n: torch.zeros_like(t, device=dev) for n, t in cpu.items()}
-    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * len(names), fresh, host, staging_bytes=512 << 10)
+    ctx2 = kv_io.KVIOContext(names, groups, bpb, [pf] * len(names), fresh, host, staging_bytes=256 << 10)
     got = {}
     loader = threading.Thread(target=lambda: got.setdefault("saved", ctx2.load(offs, blocks)))
     loader.start()

@@ -63,7 +63,7 @@ def test_request_lifecycle(dev):
     src_dev = {n: t.to(dev) for n, t in zip(names, src)}
     bpb = [2 * PS * H * D * 2] * L
     host = torch.zeros(16 << 20, dtype=torch.uint8, pin_memory=True)
-    store = kv_io.KVIOContext(names, [0] * L, bpb, [False] * L, src_dev, host, staging_bytes=8 << 20)
+    store = kv_io.KVIOContext(names, [0] * L, bpb, [False] * L, src_dev, host, staging_bytes=4 << 20)
     offs, pos = [], 4096
     for b in src_blocks:
         offs.append(pos)
@@ -78,7 +78,7 @@ def test_request_lifecycle(dev):
     req_pages = group_ptr[-1] // PS
     req_blocks = ids[o:o + req_pages].tolist()           # the request's own blocks (fresh ids)
     dst = {n: torch.zeros(2, NB, PS, H, D, dtype=torch.bfloat16, device=dev) for n in names}
-    load = kv_io.KVIOContext(names, [0] * L, bpb, [False] * L, dst, host, staging_bytes=8 << 20)
+    load = kv_io.KVIOContext(names, [0] * L, bpb, [False] * L, dst, host, staging_bytes=4 << 20)
     load_blocks, new_pos = [], []
     for c in range(3):
         first = group_ptr[c + 1] // PS
