@@ -978,10 +978,10 @@ int scatter_rerotate(daric_copier* c, const char* const* names, int64_t n_jobs, 
             }
             // Job sets too large to travel inline are read by the fused
             // kernels straight from the pinned slot (one 80-byte read per
-            // 32 KiB workgroup): no upload kernel and no dependency gap before
-            // them, ~4 us less per call on MI355X. The copy kernels keep the
-            // upload: their 8 KiB workgroups are 4x as many, and reading over
-            // the host link cost the gather ~5 us.
+            // workgroup of at least 16 KiB): no upload kernel and no
+            // dependency gap before them, ~4 us less per call on MI355X. The
+            // copy kernels keep the upload: their 8 KiB workgroups are more,
+            // and reading over the host link cost the gather ~5 us.
             DescHandOver ho(r.device, gr.jobs.data(), bytes, st, true);
             launch_scatter_rotate(ho.arg(), static_cast<int>(gr.jobs.size()), static_cast<int>(gr.max_tiles),
                                   gd, gr.kind, rope->is_neox != 0, rope->inv_freq, st);
