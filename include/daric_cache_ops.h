@@ -23,7 +23,9 @@
  *  - A call whose job descriptors fit in 2816 bytes passes them in the kernel
  *    arguments and enqueues only kernels, so it may be recorded by a HIP
  *    stream capture. A larger call stages them in a per-device ring of pinned
- *    slots and returns DARIC_ERR_INVALID while `stream` is capturing.
+ *    slots and returns DARIC_ERR_INVALID while `stream` is capturing, except
+ *    daric_copier_scatter_pages_rerotate_noalloc, which stages them in a
+ *    static device array and may be captured.
  */
 #ifndef DARIC_CACHE_OPS_H
 #define DARIC_CACHE_OPS_H
