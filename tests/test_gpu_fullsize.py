@@ -235,6 +235,34 @@ def test_config3_full_size(dev):
 
 
 @pytest.mark.timeout(900)
+@pytest.mark.parametrize("config", [3, 5])
+def test_select_merge_full_size(dev, config):
+    """select_merge, the selection step bench.py times (config 3: the
+    deviation kernel, then each (layer, chunk)'s top-k and merge fused in one
+    workgroup; config 5: the three kernels, its chunks' selected rows being
+    too many for one workgroup), against the three separate calls on a copy
+    of the same cache at full size: keys, indices and every merged cache byte
+    identical. The three calls are held to the oracle on every layer by
+    test_config3_full_size and test_config5_full_size."""
+    bench = _bench()
+    w = bench.config3_inputs(dev) if config == 3 else bench.config5_inputs(dev)
+    layers = w["layers"] if config == 3 else w["cache"]
+    L, k = w["L"], w["k"]
+    bt, chunks, k_new, v_new = w["bt"], w["chunks"], w["k_new"], w["v_new"]
+    ks, vs = (None, None) if config == 3 else (w["k_scales"], w["v_scales"])
+    twin = [t.clone() for t in layers]
+    keys3 = cache_ops.kv_deviation(twin, False, bt, k_new, chunks, k_scales=ks)
+    sel3 = cache_ops.topk_per_chunk(keys3, chunks, kmax=k)
+    cache_ops.merge_rows(twin, False, bt, k_new, v_new, chunks, sel3, k_scales=ks, v_scales=vs)
+    keys, sel = cache_ops.select_merge(layers, False, bt, k_new, v_new, chunks, kmax=k, k_scales=ks, v_scales=vs)
+    torch.cuda.synchronize()
+    assert torch.equal(keys.view(torch.int32), keys3.view(torch.int32)), "keys differ"
+    assert torch.equal(sel, sel3), "indices differ"
+    for l in range(L):
+        assert torch.equal(layers[l].view(torch.uint8), twin[l].view(torch.uint8)), f"merge of layer {l}"
+
+
+@pytest.mark.timeout(900)
 def test_config4_store_load_full_size(dev):
     """Config 4 at full size: KVIOContext stores the 65536 tokens (64 records
     of 1024 tokens, 32 layers) of bench.config4_inputs into pinned host
