@@ -235,6 +235,61 @@ def test_config3_full_size(dev):
 
 
 @pytest.mark.timeout(900)
+def test_config2_hnd_token_copies_full_size(dev):
+    """Config 2's return path on a head-major cache at full size (bench's
+    config2h: 32 layers of [2, 65536, 16, 8, 128] bf16 stored HND, 128 GiB,
+    8192 tokens on 512 random pages): gather_tokens writes exactly the
+    token-major rows torch indexing reads from the same pages, and
+    scatter_tokens of changed rows rewrites exactly those pages' K and V
+    rows, every other page of the cache keeping its bytes (checked through a
+    checksum of all pages)."""
+    bench = _bench()
+    c = bench.CFG2
+    L, H, D, PS, NB = c["layers"], c["kv_heads"], c["head_dim"], c["block_size"], c["num_blocks"]
+    T = c["chunks"] * c["chunk_tokens"]
+    n_pages = T // PS
+    g = torch.Generator().manual_seed(0)
+    ids = (torch.randperm(NB - 1, generator=g)[:n_pages] + 1).to(torch.int32).to(dev)
+    gd = torch.Generator(device=dev).manual_seed(1)
+    cache = []
+    for _ in range(L):
+        t = torch.empty(2, NB, H, PS, D, device=dev, dtype=torch.int16)
+        t.random_(generator=gd)
+        cache.append(t.view(torch.bfloat16).permute(0, 1, 3, 2, 4))
+    names = [f"model.layers.{i}.self_attn.attn" for i in range(L)]
+    per_layer = 2 * T * H * D * 2
+    staging = torch.zeros(L * per_layer, dtype=torch.uint8, device=dev)
+    cp = cache_ops.CacheCopier()
+    for n, t in zip(names, cache):
+        cp.register_layer(n, t, False)
+    cp.register_store(staging)
+    flat = ids.repeat(L)
+    args = (names, [i * per_layer for i in range(L)], [per_layer] * L, flat,
+            [i * n_pages for i in range(L + 1)])
+    cp.gather_tokens(*args)
+    torch.cuda.synchronize()
+    rows = staging.view(L, 2, T, H, D * 2)
+    for l in range(L):
+        want = cache[l][:, ids.long()].reshape(2, T, H, D)           # [2, pages, PS, H, D] token-major
+        assert torch.equal(rows[l].view(torch.int16).view(2, T, H, D), want.view(torch.int16)), f"layer {l}"
+    # scatter changed rows back: exactly the listed pages change
+    def page_sums():
+        return torch.stack([t.view(torch.int16).sum(dim=(0, 2, 3, 4), dtype=torch.int64) for t in cache])
+    before = page_sums()
+    staging.view(torch.int16).bitwise_not_()
+    cp.scatter_tokens(*args)
+    torch.cuda.synchronize()
+    for l in range(L):
+        want = rows[l].view(torch.int16).view(2, T, H, D)
+        got = cache[l][:, ids.long()].reshape(2, T, H, D).view(torch.int16)
+        assert torch.equal(got, want), f"scatter, layer {l}"
+    after = page_sums()
+    listed = torch.zeros(NB, dtype=torch.bool, device=dev)
+    listed[ids.long()] = True
+    assert torch.equal(after[:, ~listed], before[:, ~listed]), "pages outside the list changed"
+
+
+@pytest.mark.timeout(900)
 @pytest.mark.parametrize("config", [3, 5])
 def test_select_merge_full_size(dev, config):
     """select_merge, the selection step bench.py times (config 3: the
