@@ -203,6 +203,57 @@ def test_config2_full_size_properties(dev):
 
 
 @pytest.mark.timeout(900)
+def test_config2_inplace_full_size(dev):
+    """The worker-side form at config 2's full size (the call bench.py times
+    as rerotate_inplace): the staged pages scattered unrotated, then
+    rerotate_pages moves chunks 1..7 in all 32 layers in place (the Adapter's
+    call); gathered back, V and chunk 0 are bit-exact and every rotated K
+    element is within the rotation bar of the fp64 rotation, with no allowance
+    outside near-cancellations."""
+    bench = _bench()
+    cfg = bench.CFG2
+    w = bench.build_workload(cfg, dev)
+    j = w["jobs"]
+    H, D, CT = cfg["kv_heads"], cfg["head_dim"], cfg["chunk_tokens"]
+    cp = cache_ops.CacheCopier()
+    for n, t in zip(w["names"], w["cache"]):
+        cp.register_layer(n, t, False)
+    cp.register_store(w["staging"])
+    idx = torch.tensor(j["flat"], dtype=torch.int32, device=dev)
+    inv = w["inv_freq"].to(dev)
+    cp.scatter_pages(j["names"], j["offsets"], j["sizes"], idx, j["ioff"])
+    pages = CT // cfg["block_size"]
+    segs = [(c * pages, 0, CT, c * CT) for c in range(1, cfg["chunks"])]
+    cache_ops.rerotate_pages(w["cache"], False, w["ids"].to(dev), segs, inv, D, True)
+    back = torch.zeros_like(w["staging"])
+    gp = cache_ops.CacheCopier()
+    for n, t in zip(w["names"], w["cache"]):
+        gp.register_layer(n, t, False)
+    gp.register_store(back)
+    gp.gather_pages(j["names"], j["offsets"], j["sizes"], idx, j["ioff"])
+    torch.cuda.synchronize()
+    n_jobs = len(j["offsets"])
+    src = w["staging"].view(torch.bfloat16).view(n_jobs, 2, CT, H, D)
+    got = back.view(torch.bfloat16).view(n_jobs, 2, CT, H, D)
+    assert torch.equal(got[:, 1].view(torch.int16), src[:, 1].view(torch.int16)), "V bytes differ"
+    deltas = torch.tensor(j["deltas"], device=dev)
+    still = deltas == 0
+    assert torch.equal(got[still, 0].view(torch.int16), src[still, 0].view(torch.int16)), "chunk 0 K differs"
+    moved = (~still).nonzero().flatten()
+    assert moved.numel() == 224
+    for part in moved.split(16):
+        k_in, k_out = src[part, 0].double(), got[part, 0].double()
+        want = _rotate64(k_in, deltas[part], inv)
+        x1, x2 = k_in[..., : D // 2], k_in[..., D // 2:]
+        norm = torch.sqrt(x1 ** 2 + x2 ** 2).repeat(1, 1, 1, 2)
+        one_ulp = _bf16_ulp(torch.maximum(want.abs(), k_out.abs()))
+        err = (k_out - want).abs()
+        assert bool((err <= one_ulp + 2.0 ** -20 * norm).all()), f"jobs {part.tolist()[:3]}.."
+        plain = want.abs() >= 2.0 ** -10 * norm
+        assert bool((err[plain] <= one_ulp[plain]).all()), f"jobs {part.tolist()[:3]}..: beyond 1 ulp"
+
+
+@pytest.mark.timeout(900)
 def test_config3_full_size(dev):
     """Config 3 at full size, on the bench's own inputs (bench.config3_inputs:
     32 layers x 98304 tokens in 192 shuffled chunks, k = 77): deviation keys
