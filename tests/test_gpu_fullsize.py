@@ -376,7 +376,9 @@ def test_config4_store_load_full_size(dev):
     layer's pages in the reference's [K|V][pages][span] layout with the int64
     saved position at the head of each 4096-byte header; the loaded pages are
     byte-identical, every other page stays zero, and load returns the saved
-    positions."""
+    positions. The fused re-rotating load of the same records moves record m
+    by m * 1024 positions: V bit-exact, record 0 unchanged, every moved K
+    element within the rotation bar of the fp64 rotation."""
     from daric_amd.kv_io import KVIOContext
     bench = _bench()
     w = bench.config4_inputs(dev)
@@ -411,6 +413,30 @@ def test_config4_store_load_full_size(dev):
     for a, b in zip(cache, cache2):
         assert torch.equal(b[:, ids].view(torch.int16), a[:, ids].view(torch.int16))
         assert not bool(b[:, untouched].view(torch.int16).any())
+    del io2, cache2
+    # the fused re-rotating load (bench.py's load_pipeline_fused): record m's
+    # 1024 tokens move from their saved position by m * 1024 (record 0 stays)
+    cache3 = [torch.zeros_like(t) for t in cache]
+    io3 = KVIOContext(names, [0] * L, plan["bpb"], [False] * L, dict(zip(names, cache3)), host,
+                      staging_bytes=512 << 20)
+    H, D = w["H"], w["D"]
+    inv = (1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))).to(dev)
+    M = len(blocks)
+    new_pos = [positions[m] + m * 1024 for m in range(M)]
+    assert io3.load(plan["offsets"], blocks, rerotate=(new_pos, [1024] * M, inv, D, True)) == positions
+    io3.done.synchronize()
+    deltas = torch.arange(M, device=dev) * 1024
+    for a, b in zip(cache, cache3):
+        assert torch.equal(b[1, ids].view(torch.int16), a[1, ids].view(torch.int16)), "V differs"
+        assert not bool(b[:, untouched].view(torch.int16).any())
+        k_in = a[0, ids].double().reshape(M, 1024, H, D)
+        k_out = b[0, ids].double().reshape(M, 1024, H, D)
+        assert torch.equal(k_out[0], k_in[0]), "record 0 moved"
+        want = _rotate64(k_in, deltas, inv)
+        x1, x2 = k_in[..., : D // 2], k_in[..., D // 2:]
+        norm = torch.sqrt(x1 ** 2 + x2 ** 2).repeat(1, 1, 1, 2)
+        err = (k_out - want).abs()
+        assert bool((err <= _bf16_ulp(torch.maximum(want.abs(), k_out.abs())) + 2.0 ** -20 * norm).all())
 
 
 @pytest.mark.timeout(900)
