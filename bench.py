@@ -534,10 +534,14 @@ def run_config4(steps, warmup, seed=0):
         torch.cuda.synchronize()
         return ev0.elapsed_time(ev1)
 
+    # one untimed copy each way first, then the median of n_host timed copies
     host_copy(True)
+    host_copy(False)
     n_host = max(1, min(steps, 3))
-    d2h_ms = float(np.median([host_copy(True) for _ in range(n_host)]))
-    h2d_ms = float(np.median([host_copy(False) for _ in range(n_host)]))
+    d2h_runs = [host_copy(True) for _ in range(n_host)]
+    h2d_runs = [host_copy(False) for _ in range(n_host)]
+    d2h_ms = float(np.median(d2h_runs))
+    h2d_ms = float(np.median(h2d_runs))
     dev_bytes = 2 * L * per_layer
     link_bytes = L * per_layer
     # the store/load pipeline: 64 records of 1024 tokens, gather/scatter overlapped with host DMA
@@ -607,8 +611,8 @@ def run_config4(steps, warmup, seed=0):
                             GBps=_gbps(dev_bytes, scatter["kern_ms"]),
                             frac=_gbps(dev_bytes, scatter["kern_ms"]) / PEAK_HBM_GBPS),
                device_algorithmic_bytes=dev_bytes,
-               d2h=dict(ms=d2h_ms, GBps=_gbps(link_bytes, d2h_ms)),
-               h2d=dict(ms=h2d_ms, GBps=_gbps(link_bytes, h2d_ms)),
+               d2h=dict(ms=d2h_ms, GBps=_gbps(link_bytes, d2h_ms), runs_ms=[round(x, 3) for x in d2h_runs]),
+               h2d=dict(ms=h2d_ms, GBps=_gbps(link_bytes, h2d_ms), runs_ms=[round(x, 3) for x in h2d_runs]),
                host_link_bytes=link_bytes,
                store_pipeline=dict(ms=store_ms, GBps=_gbps(link_bytes, store_ms),
                                    tokens_per_s=T / (store_ms / 1e3)),
