@@ -713,6 +713,14 @@ def run_config5(steps, warmup, seed=0):
     # pattern's copy rate on this box
     pattern = time_steps(lambda: cp.scatter_pages(j["names"], j["offsets"], j["sizes"], w["idx"], j["ioff"], st),
                          steps, 1, stream)
+    # the worker's form on the fp8 cache, the reference's own fp8 rotation
+    # (adapter.py:370-373, in place on the e4m3 view): rerotate_pages of chunks
+    # 1..15 in all 80 layers (chunk 0 does not move); K codes read and written
+    CT, PS = w["CT"], w["PS"]
+    segs = [(ci * (CT // PS), 0, CT, ci * CT) for ci in range(1, C)]
+    inplace = time_steps(lambda: cache_ops.rerotate_pages(cache, False, w["bt"], segs, w["inv"], D, True,
+                                                          stream=st), steps, 1, stream)
+    inplace_bytes = (C - 1) * CT * L * 2 * H * D * 1
     # selection on the fp8 cache: recomputed K (bf16) vs the dequantised cached
     # K, top-10%, then the selected bf16 K/V rows quantised into the cache
     bt, chunks, k_new, v_new = w["bt"], w["chunks"], w["k_new"], w["v_new"]
@@ -766,6 +774,13 @@ def run_config5(steps, warmup, seed=0):
                pattern_copy=dict(kernel="copy_pages_kernel<16,scatter> on the same 1280 jobs, no rotation",
                                  kernel_ms=pattern["kern_ms"], GBps=_gbps(fused_bytes, pattern["kern_ms"]),
                                  fused_frac_of_it=pattern["kern_ms"] / fused["kern_ms"]),
+               rerotate_inplace=dict(ms_per_step=inplace["step_ms"], kernel_ms=inplace["kern_ms"],
+                                     algorithmic_bytes=inplace_bytes,
+                                     GBps=_gbps(inplace_bytes, inplace["kern_ms"]),
+                                     frac=_gbps(inplace_bytes, inplace["kern_ms"]) / PEAK_HBM_GBPS,
+                                     tokens_per_s=(C - 1) * CT / (inplace["step_ms"] / 1e3),
+                                     note="rerotate_pages of chunks 1..15 in all 80 layers of the e4m3 "
+                                          "cache (in place, the Adapter's call): K codes read and written"),
                selection=dict(k=k, ms_per_step=selection["step_ms"], algorithmic_bytes=sel_bytes,
                               GBps=_gbps(sel_bytes, selection["step_ms"]),
                               step_forms=dict(ms=forms, note="as for config 3: select_merge (the step above), "

@@ -157,9 +157,19 @@ template <typename T>
 __device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
 
 constexpr int kLaneUnroll = 2;
+// e4m3: 4 units in flight per lane, so a workgroup holds a whole 16 KiB K page
+// of the Llama-3-70B shape in one round.
+constexpr int kLaneUnrollFp8 = 4;
 
-
-template <int KIND, bool NEOX>
+// CSL (e4m3): a lane reads its cos/sin values from LDS at each use instead of
+// holding them in registers. A 16-byte e4m3 unit spans 16 pairs: held in
+// registers they took the kernel to 96 VGPRs (5 waves/SIMD); read from LDS as
+// (cos, sin) float4s of two pairs, as the fused kernel does, it takes 50. With
+// kLaneUnrollFp8 it ran the config-5 in-place call (15 chunks x 2048 tokens x
+// 80 layers) in 1018 against 1033 us, at the rate of the same kernel with the
+// rotation taken out (1015 us, a pure read-modify-write of the same pages), in
+// a same-process A/B on MI355X. Both forms give identical bits.
+template <int KIND, bool NEOX, bool CSL, int UNR>
 __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
     DescArg d, int layer_off, int layer0, InplaceGeom g, int n_segs,
     const int32_t* __restrict__ bt, const float* __restrict__ inv_freq, FastDiv d_tok, FastDiv d_ps,
@@ -168,9 +178,10 @@ __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
     constexpr int VE = E::VE;
     constexpr int EPW = E::EPW;
     constexpr int ES = KIND == kE4M3 ? 1 : 2;
-    constexpr int NC = NEOX ? VE : VE / 2;   // cos/sin values per lane
+    constexpr int NC = CSL ? 1 : (NEOX ? VE : VE / 2);   // cos/sin values per lane in registers
     __shared__ float s_cos[kMaxHalfRot];
     __shared__ float s_sin[kMaxHalfRot];
+    __shared__ float4 s_cs[kMaxHalfRot / 2];   // CSL: (cos, sin) of two pairs per entry
 
     const DescPtr<RopeSeg> segs = desc_at<RopeSeg>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off) + layer0;
@@ -202,11 +213,11 @@ __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
     const int half = g.R / 2;
 
     float cs[NC], ss[NC];
-    for (int base = u0; base < u1; base += kThreads * kLaneUnroll) {
-        u32x4 v[kLaneUnroll];
-        bool act[kLaneUnroll];
+    for (int base = u0; base < u1; base += kThreads * UNR) {
+        u32x4 v[UNR];
+        bool act[UNR];
 #pragma unroll
-        for (int u = 0; u < kLaneUnroll; ++u) {
+        for (int u = 0; u < UNR; ++u) {
             const int i = base + u * kThreads + tid;
             const uint32_t r = static_cast<uint32_t>(i >> log2_upr);
             const uint32_t q = d_tok.div(r);
@@ -221,25 +232,44 @@ __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
             // the lanes of a wavefront read consecutive words for each e
             // (row-major, the stride-NC reads took 2-way bank conflicts:
             // 30% of the kernel's LDS cycles at config 2).
+            // CSL: the (cos, sin) entries are transposed the same way -- NeoX
+            // float4 j (pairs 2j, 2j+1 of a unit) of unit kk at
+            // j * (half / VE) + kk, GPT-J float2 pair pi at
+            // pi * (half / (VE / 2)) + kk -- so each LDS read takes
+            // consecutive entries across the lanes.
             const int cols = half / NC;
             for (int i = tid; i < half; i += kThreads) {
                 float sn, c;
                 sincosf(sg.delta * inv_freq[i], &sn, &c);
-                const int at = (i % NC) * cols + i / NC;
-                s_cos[at] = c;
-                s_sin[at] = sn;
+                if constexpr (CSL) {
+                    float* q;
+                    if (NEOX) {
+                        const int f = i >> 1;
+                        q = reinterpret_cast<float*>(s_cs + (f % (VE / 2)) * (half / VE) + f / (VE / 2)) + 2 * (i & 1);
+                    } else {
+                        q = reinterpret_cast<float*>(s_cs) + 2 * ((i % (VE / 2)) * (half / (VE / 2)) + i / (VE / 2));
+                    }
+                    q[0] = c;
+                    q[1] = sn;
+                } else {
+                    const int at = (i % NC) * cols + i / NC;
+                    s_cos[at] = c;
+                    s_sin[at] = sn;
+                }
             }
             __syncthreads();
-            const int kk = pi0 / NC;
+            if constexpr (!CSL) {
+                const int kk = pi0 / NC;
 #pragma unroll
-            for (int e = 0; e < NC; ++e) {
-                const int at = rot_lane ? e * cols + kk : 0;
-                cs[e] = s_cos[at];
-                ss[e] = (NEOX && first) ? -s_sin[at] : s_sin[at];
+                for (int e = 0; e < NC; ++e) {
+                    const int at = rot_lane ? e * cols + kk : 0;
+                    cs[e] = s_cos[at];
+                    ss[e] = (NEOX && first) ? -s_sin[at] : s_sin[at];
+                }
             }
         }
 #pragma unroll
-        for (int u = 0; u < kLaneUnroll; ++u) {
+        for (int u = 0; u < UNR; ++u) {
             u32x4 pv = v[u];
             if (NEOX) {
 #pragma unroll
@@ -255,16 +285,38 @@ __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
                 if (NEOX) {
                     float y[EPW];
                     E::unpack_word(pv[w], y);
+                    if constexpr (CSL) {
+                        // pairs pi0 + w*EPW .. +EPW-1: EPW/2 float4 reads
+                        const int kk = pi0 / VE;
 #pragma unroll
-                    for (int e = 0; e < EPW; ++e)
-                        x[e] = x[e] * cs[w * EPW + e] + y[e] * ss[w * EPW + e];
+                        for (int h2 = 0; h2 < EPW / 2; ++h2) {
+                            const float4 t = s_cs[(w * (EPW / 2) + h2) * (half / VE) + kk];
+                            const float s0 = first ? -t.y : t.y, s1 = first ? -t.w : t.w;
+                            x[2 * h2] = x[2 * h2] * t.x + y[2 * h2] * s0;
+                            x[2 * h2 + 1] = x[2 * h2 + 1] * t.z + y[2 * h2 + 1] * s1;
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < EPW; ++e)
+                            x[e] = x[e] * cs[w * EPW + e] + y[e] * ss[w * EPW + e];
+                    }
                 } else {
 #pragma unroll
                     for (int m = 0; m < EPW / 2; ++m) {
                         const int pi = w * (EPW / 2) + m;
+                        float c, sn;
+                        if constexpr (CSL) {
+                            const float* csq = reinterpret_cast<const float*>(s_cs) +
+                                               2 * (pi * (half / (VE / 2)) + pi0 / (VE / 2));
+                            c = csq[0];
+                            sn = csq[1];
+                        } else {
+                            c = cs[pi];
+                            sn = ss[pi];
+                        }
                         const float x1 = x[2 * m], x2 = x[2 * m + 1];
-                        x[2 * m] = x1 * cs[pi] - x2 * ss[pi];
-                        x[2 * m + 1] = x2 * cs[pi] + x1 * ss[pi];
+                        x[2 * m] = x1 * c - x2 * sn;
+                        x[2 * m + 1] = x2 * c + x1 * sn;
                     }
                 }
                 out[w] = E::pack_word(x);
@@ -342,7 +394,7 @@ void launch_rerotate_inplace(const DescArg& d, int layer_off, int n_layers, cons
         const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(nl));
 #define DARIC_RV(K, N) DARIC_LAUNCH((rerotate_vec_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq, d_tok, d_rot, d_ps)
 #define DARIC_RE(K, N) DARIC_LAUNCH((rerotate_elem_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq)
-#define DARIC_RL(K, N) DARIC_LAUNCH((rerotate_lane_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq, d_ltok, d_ps, g.log2_parts)
+#define DARIC_RL(K, N) DARIC_LAUNCH((rerotate_lane_kernel<K, N, K == kE4M3, K == kE4M3 ? kLaneUnrollFp8 : kLaneUnroll>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq, d_ltok, d_ps, g.log2_parts)
         if (path == kRotLane) {
             if (kind == kBF16) { if (neox) DARIC_RL(kBF16, true); else DARIC_RL(kBF16, false); }
             else if (kind == kF16) { if (neox) DARIC_RL(kF16, true); else DARIC_RL(kF16, false); }

@@ -503,3 +503,47 @@ def test_config5_full_size(dev):
                         sel_np[l:l + 1], k_scales=ks[l:l + 1], v_scales=vs[l:l + 1])
         assert torch.equal(w["cache"][l].cpu(), pre[l]), f"merge of layer {l}"
         del pre[l]
+
+
+@pytest.mark.timeout(900)
+def test_config5_inplace_full_size(dev):
+    """The worker-side fp8 form at config 5's full size (the call bench.py
+    times as config5.rerotate_inplace, the reference's own fp8 rotation on the
+    e4m3 view, adapter.py:370-373): the staged codes scattered unrotated, then
+    rerotate_pages moves chunks 1..15 in all 80 layers in place; gathered
+    back, V codes and chunk 0 are bit-exact and every moved K code is within 1
+    e4m3 quantum of the float64 rotation of the decoded staged code (saturated
+    at 448)."""
+    bench = _bench()
+    w = bench.config5_inputs(dev)
+    L, H, D, C, CT, PS = w["L"], w["H"], w["D"], w["C"], w["CT"], w["PS"]
+    j = w["jobs"]
+    cp = cache_ops.CacheCopier()
+    for n, t in zip(w["names"], w["cache"]):
+        cp.register_layer(n, t, False)
+    cp.register_store(w["staging"])
+    cp.scatter_pages(j["names"], j["offsets"], j["sizes"], w["idx"], j["ioff"])
+    segs = [(c * (CT // PS), 0, CT, c * CT) for c in range(1, C)]
+    cache_ops.rerotate_pages(w["cache"], False, w["bt"], segs, w["inv"], D, True, k_scales=w["k_scales"])
+    back = torch.zeros_like(w["staging"])
+    gp = cache_ops.CacheCopier()
+    for n, t in zip(w["names"], w["cache"]):
+        gp.register_layer(n, t, False)
+    gp.register_store(back)
+    gp.gather_pages(j["names"], j["offsets"], j["sizes"], w["idx"], j["ioff"])
+    torch.cuda.synchronize()
+    n_jobs = len(j["offsets"])
+    assert n_jobs == C * L and j["offsets"] == [i * w["job_bytes"] for i in range(n_jobs)]
+    src = w["staging"].view(n_jobs, 2, CT, H, D)
+    got = back.view(n_jobs, 2, CT, H, D)
+    assert torch.equal(got[:, 1], src[:, 1]), "V codes differ"
+    assert torch.equal(got[:L, 0], src[:L, 0]), "chunk 0 K codes differ"
+    deltas = torch.tensor(j["deltas"], device=dev)
+    for c in range(1, C):
+        for part in torch.arange(c * L, (c + 1) * L, device=dev).split(20):
+            k_in = src[part, 0].view(torch.float8_e4m3fn).float().double()
+            k_out = got[part, 0].view(torch.float8_e4m3fn).float().double()
+            want = _rotate64(k_in, deltas[part], w["inv"]).clamp(-448.0, 448.0)
+            tol = _e4m3_quantum(torch.maximum(want.abs(), k_out.abs()))
+            ratio = float(((k_out - want).abs() / tol).max())
+            assert ratio <= 1.0, f"chunk {c}: worst {ratio:.2f} e4m3 quanta"
