@@ -1,6 +1,7 @@
 // Launchers of the gfx950 kernels (defined in the .hip files).
 #pragma once
 
+#include <algorithm>
 #include <mutex>
 
 #include <hip/hip_runtime_api.h>
@@ -35,6 +36,51 @@ struct RowGeomDiv {
     RowGeom g;
     FastDiv ipr, tok_div, ps;
 };
+
+// Layer-minor block order for kernels over (layer, work item) pairs: block b
+// of a launch takes layer l0 + b % nl and work item w0 + b / nl. Workgroups
+// are dispatched to the 8 XCDs in turn, so with nl a multiple of 8 each XCD
+// works on a fixed eighth of the layers, and its address translations and L2
+// see an eighth of the layers' memory. On MI355X that made the row merge 8-12%
+// faster, the fused top-k + merge 5-7% and the in-place re-rotation 4-10%
+// than work-item-major grids (in same-process A/Bs at configs 2, 3 and 5);
+// the deviation kernel, which streams each layer's rows in order, ran 4-5%
+// slower that way and keeps its tile-major grid.
+struct LayerMinor {
+    int32_t l0 = 0;     // first layer of the launch
+    int32_t nl = 1;     // layers of the launch
+    int64_t w0 = 0;     // first work item of the launch
+#ifdef __HIPCC__
+    __device__ inline void at(int& l, int64_t& w) const {
+        const uint32_t b = blockIdx.x;
+        const uint32_t n = static_cast<uint32_t>(nl);
+        l = l0 + static_cast<int>(b % n);
+        w = w0 + static_cast<int64_t>(b / n);
+    }
+#endif
+};
+
+// Largest grid.x of a 256-lane launch (grid.x * 256 lanes < 2^32).
+constexpr int64_t kMaxGridBlocks = (1ll << 24) - 1;
+
+// Calls launch(LayerMinor, blocks) for launches that together cover
+// n_layers x n_items, each of at most kMaxGridBlocks blocks.
+template <class F>
+void for_layer_minor(int n_layers, int64_t n_items, F&& launch) {
+    if (n_layers <= 0 || n_items <= 0) return;
+    const int64_t nl = std::min<int64_t>(n_layers, kMaxGridBlocks);
+    const int64_t per = std::max<int64_t>(1, kMaxGridBlocks / nl);
+    for (int64_t l0 = 0; l0 < n_layers; l0 += nl) {
+        LayerMinor lm;
+        lm.l0 = static_cast<int32_t>(l0);
+        lm.nl = static_cast<int32_t>(std::min<int64_t>(nl, n_layers - l0));
+        for (int64_t w0 = 0; w0 < n_items; w0 += per) {
+            lm.w0 = w0;
+            const int64_t ni = std::min<int64_t>(per, n_items - w0);
+            launch(lm, static_cast<unsigned>(lm.nl * ni));
+        }
+    }
+}
 
 // XCD-aware unit order for grids whose consecutive units write consecutive
 // bytes (the gathers: staging is the contiguous side). Workgroups are

@@ -171,7 +171,7 @@ constexpr int kLaneUnrollFp8 = 4;
 // a same-process A/B on MI355X. Both forms give identical bits.
 template <int KIND, bool NEOX, bool CSL, int UNR>
 __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
-    DescArg d, int layer_off, int layer0, InplaceGeom g, int n_segs,
+    DescArg d, int layer_off, LayerMinor lm, InplaceGeom g, int n_segs,
     const int32_t* __restrict__ bt, const float* __restrict__ inv_freq, FastDiv d_tok, FastDiv d_ps,
     int log2_parts) {
     using E = Elem<KIND>;
@@ -184,8 +184,11 @@ __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
     __shared__ float4 s_cs[kMaxHalfRot / 2];   // CSL: (cos, sin) of two pairs per entry
 
     const DescPtr<RopeSeg> segs = desc_at<RopeSeg>(d, 0);
-    const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off) + layer0;
-    const int tile = static_cast<int>(blockIdx.x);
+    const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
+    int lyr;
+    int64_t w;
+    lm.at(lyr, w);
+    const int tile = static_cast<int>(w);
     const RopeSeg sg = desc_load(segs + find_segment(segs, n_segs, tile));
     if (sg.delta == 0.0f) return;
     const int page = sg.tok_start / g.PS + ((tile - sg.tile_begin) >> log2_parts);
@@ -196,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
     if (hi <= lo) return;
     const int blk = bt[sg.bt_offset + page];
     if (blk < g.min_block || blk >= g.num_blocks) return;
-    u32x4* __restrict__ pg = reinterpret_cast<u32x4*>(layers[blockIdx.y] + static_cast<int64_t>(blk) * g.sb * ES);
+    u32x4* __restrict__ pg = reinterpret_cast<u32x4*>(layers[lyr] + static_cast<int64_t>(blk) * g.sb * ES);
 
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & 63;
@@ -389,17 +392,24 @@ void launch_rerotate_inplace(const DescArg& d, int layer_off, int n_layers, cons
     constexpr int kMaxY = 65535;
     const FastDiv d_tok(static_cast<uint32_t>(g.H * g.n_rot)), d_rot(static_cast<uint32_t>(g.n_rot)),
         d_ps(static_cast<uint32_t>(g.PS)), d_ltok(static_cast<uint32_t>(g.tok_div > 0 ? g.tok_div : 1));
+    if (path == kRotLane) {
+        // one workgroup per (layer, page part), layer-minor
+        for_layer_minor(n_layers, n_tiles, [&](const LayerMinor& lm, unsigned blocks) {
+#define DARIC_RL(K, N) DARIC_LAUNCH((rerotate_lane_kernel<K, N, K == kE4M3, K == kE4M3 ? kLaneUnrollFp8 : kLaneUnroll>), blocks, kThreads, 0, stream, d, layer_off, lm, g, n_segs, block_table, inv_freq, d_ltok, d_ps, g.log2_parts)
+            if (kind == kBF16) { if (neox) DARIC_RL(kBF16, true); else DARIC_RL(kBF16, false); }
+            else if (kind == kF16) { if (neox) DARIC_RL(kF16, true); else DARIC_RL(kF16, false); }
+            else { if (neox) DARIC_RL(kE4M3, true); else DARIC_RL(kE4M3, false); }
+#undef DARIC_RL
+            check_launch("rerotate_pages");
+        });
+        return;
+    }
     for (int l0 = 0; l0 < n_layers; l0 += kMaxY) {
         const int nl = n_layers - l0 < kMaxY ? n_layers - l0 : kMaxY;
         const dim3 grid(static_cast<unsigned>(n_tiles), static_cast<unsigned>(nl));
 #define DARIC_RV(K, N) DARIC_LAUNCH((rerotate_vec_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq, d_tok, d_rot, d_ps)
 #define DARIC_RE(K, N) DARIC_LAUNCH((rerotate_elem_kernel<K, N>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq)
-#define DARIC_RL(K, N) DARIC_LAUNCH((rerotate_lane_kernel<K, N, K == kE4M3, K == kE4M3 ? kLaneUnrollFp8 : kLaneUnroll>), grid, kThreads, 0, stream, d, layer_off, l0, g, n_segs, block_table, inv_freq, d_ltok, d_ps, g.log2_parts)
-        if (path == kRotLane) {
-            if (kind == kBF16) { if (neox) DARIC_RL(kBF16, true); else DARIC_RL(kBF16, false); }
-            else if (kind == kF16) { if (neox) DARIC_RL(kF16, true); else DARIC_RL(kF16, false); }
-            else { if (neox) DARIC_RL(kE4M3, true); else DARIC_RL(kE4M3, false); }
-        } else if (path == kRotVec) {
+        if (path == kRotVec) {
             if (kind == kBF16) { if (neox) DARIC_RV(kBF16, true); else DARIC_RV(kBF16, false); }
             else if (kind == kF16) { if (neox) DARIC_RV(kF16, true); else DARIC_RV(kF16, false); }
             else { if (neox) DARIC_RV(kE4M3, true); else DARIC_RV(kE4M3, false); }
@@ -410,7 +420,6 @@ void launch_rerotate_inplace(const DescArg& d, int layer_off, int n_layers, cons
         }
 #undef DARIC_RV
 #undef DARIC_RE
-#undef DARIC_RL
         check_launch("rerotate_pages");
     }
 }

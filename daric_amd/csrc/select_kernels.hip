@@ -386,8 +386,10 @@ constexpr int kMergeUnits = 8;
 // rows): 2% faster for the copy and 4-5% for the quantising merge than plain
 // accesses, in alternating processes. A same-process sweep at config 3 put 128
 // or 512 lanes, 1 to 16 units, a precomputed slot table, two groups per
-// workgroup and one-wavefront-per-token forms within +-2% of this, and the
-// merge at about 90% of a page scatter of the same bytes.
+// workgroup and one-wavefront-per-token forms within +-2% of this. The
+// layer-minor block order (LayerMinor) then took the config-3 merge from
+// 704-749 to 622-689 us in same-process A/Bs, about the rate of a page
+// scatter of the same bytes onto the same cache layers.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeMaxTok = 64;
 constexpr int kMergeCopy = 0;
@@ -487,19 +489,23 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
     const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T,
     int n_chunks, const int32_t* __restrict__ sel, int kmax, int tpb, int units,
     FastDiv d_tok_units, FastDiv d_upr, const float* __restrict__ k_scales,
-    const float* __restrict__ v_scales, int c0, int l0) {
+    const float* __restrict__ v_scales, LayerMinor lm, int64_t nbx) {
     __shared__ int64_t s_src[kMergeMaxTok];   // byte offset of the token's recomputed rows (-1: skip)
     __shared__ int64_t s_dst[kMergeMaxTok];   // byte offset of the token's K row in the layer
     const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
-    const int l = static_cast<int>(blockIdx.z) + l0;
-    const int ci = static_cast<int>(blockIdx.y) + c0;
+    // work item w = (chunk, row batch), batches of a chunk consecutive
+    int l;
+    int64_t w;
+    lm.at(l, w);
+    const int ci = static_cast<int>(w / nbx);
+    const int bx = static_cast<int>(w - static_cast<int64_t>(ci) * nbx);
     const SelChunk c = desc_load(chunks + ci);
     const int tid = static_cast<int>(threadIdx.x);
     const int ses = MODE == kMergeCopy ? ces : 2;                    // source element size
     const int64_t row_bytes = static_cast<int64_t>(g.H) * g.D * ses;
     if (tid < tpb) {
-        const int q = static_cast<int>(blockIdx.x) * tpb + tid;
+        const int q = bx * tpb + tid;
         const int j = q < min(kmax, c.k) ? sel[(static_cast<int64_t>(l) * n_chunks + ci) * kmax + q] : -1;
         merge_slot(j, c, l, g, T, row_bytes, ces, bt, &s_src[tid], &s_dst[tid]);
     }
@@ -522,7 +528,7 @@ __global__ __launch_bounds__(kThreads) void select_merge_kernel(
     const uint8_t* __restrict__ k_new, const uint8_t* __restrict__ v_new, int64_t T, int n_chunks,
     const float* __restrict__ dev_scales, float* __restrict__ keys, int32_t* __restrict__ sel, int kmax,
     int n_max, int units, FastDiv d_tok_units, FastDiv d_upr, const float* __restrict__ k_scales,
-    const float* __restrict__ v_scales, int c0, int l0) {
+    const float* __restrict__ v_scales, LayerMinor lm) {
     extern __shared__ __align__(16) uint32_t s_dyn[];   // keys, indices, then 8-byte offsets
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_digit, s_above;
@@ -533,8 +539,10 @@ __global__ __launch_bounds__(kThreads) void select_merge_kernel(
     int64_t* s_dst = s_src + kmax;
     const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
-    const int l = static_cast<int>(blockIdx.y) + l0;
-    const int ci = static_cast<int>(blockIdx.x) + c0;
+    int l;
+    int64_t w;
+    lm.at(l, w);
+    const int ci = static_cast<int>(w);
     const SelChunk c = desc_load(chunks + ci);
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & 63;
@@ -635,41 +643,44 @@ void launch_merge(const DescArg& d, int layer_off, int n_layers, const KVGeom& g
                   int64_t T, int n_chunks, const int32_t* sel_idx, int kmax, int quant_from,
                   const float* k_scales, const float* v_scales, hipStream_t stream) {
     const bool quant = quant_from >= 0;
+    if (merge_fits_rows(g, elem_size, quant)) {
+        // one workgroup per (layer, chunk, batch of tpb selected rows), layer-minor
+        const int ses = quant ? 2 : elem_size;
+        const int upr = g.D * ses / 16;                              // source units per head row
+        const int units = g.H * upr;                                 // per K (or V) token row
+        const int tok_units = (g.v_off >= 0 ? 2 : 1) * units;
+        const int tpb = std::min(kMergeMaxTok, std::max(1, kMergeThreads * kMergeUnits / tok_units));
+        const int64_t nbx = (static_cast<int64_t>(kmax) + tpb - 1) / tpb;
+        const FastDiv dtu(static_cast<uint32_t>(tok_units)), dupr(static_cast<uint32_t>(upr));
+        const bool dense = g.sh == g.D;
+        for_layer_minor(n_layers, nbx * n_chunks, [&](const LayerMinor& lm, unsigned blocks) {
+#define DARIC_MR(M, DN) DARIC_LAUNCH((merge_rows_kernel<M, DN>), blocks, kMergeThreads, 0, stream, d, layer_off, g, \
+                                     elem_size, block_table, k_new, v_new, T, n_chunks, sel_idx, kmax, tpb, units, \
+                                     dtu, dupr, k_scales, v_scales, lm, nbx)
+            if (!quant) { if (dense) DARIC_MR(kMergeCopy, true); else DARIC_MR(kMergeCopy, false); }
+            else if (quant_from == kBF16) { if (dense) DARIC_MR(kMergeFromBF16, true); else DARIC_MR(kMergeFromBF16, false); }
+            else { if (dense) DARIC_MR(kMergeFromF16, true); else DARIC_MR(kMergeFromF16, false); }
+#undef DARIC_MR
+            check_launch("merge_rows");
+        });
+        return;
+    }
     // grid.y (chunks) and grid.z (layers) are cut into slices of at most 65535
     for (int l0 = 0; l0 < n_layers; l0 += kMaxGridYZ) {
         const int nl = std::min(kMaxGridYZ, n_layers - l0);
         for (int c0 = 0; c0 < n_chunks; c0 += kMaxGridYZ) {
             const int nc = std::min(kMaxGridYZ, n_chunks - c0);
-            if (merge_fits_rows(g, elem_size, quant)) {
-                const int ses = quant ? 2 : elem_size;
-                const int upr = g.D * ses / 16;                              // source units per head row
-                const int units = g.H * upr;                                 // per K (or V) token row
-                const int tok_units = (g.v_off >= 0 ? 2 : 1) * units;
-                const int tpb = std::min(kMergeMaxTok, std::max(1, kMergeThreads * kMergeUnits / tok_units));
-                const dim3 grid(static_cast<unsigned>((kmax + tpb - 1) / tpb), static_cast<unsigned>(nc),
-                                static_cast<unsigned>(nl));
-                const FastDiv dtu(static_cast<uint32_t>(tok_units)), dupr(static_cast<uint32_t>(upr));
-                const bool dense = g.sh == g.D;
-#define DARIC_MR(M, DN) DARIC_LAUNCH((merge_rows_kernel<M, DN>), grid, kMergeThreads, 0, stream, d, layer_off, g, \
-                                     elem_size, block_table, k_new, v_new, T, n_chunks, sel_idx, kmax, tpb, units, \
-                                     dtu, dupr, k_scales, v_scales, c0, l0)
-                if (!quant) { if (dense) DARIC_MR(kMergeCopy, true); else DARIC_MR(kMergeCopy, false); }
-                else if (quant_from == kBF16) { if (dense) DARIC_MR(kMergeFromBF16, true); else DARIC_MR(kMergeFromBF16, false); }
-                else { if (dense) DARIC_MR(kMergeFromF16, true); else DARIC_MR(kMergeFromF16, false); }
-#undef DARIC_MR
-            } else {
-                const dim3 grid(static_cast<unsigned>((kmax + kMergeTok - 1) / kMergeTok), static_cast<unsigned>(nc),
-                                static_cast<unsigned>(nl));
-                const bool vec = (g.D * elem_size) % 16 == 0 && (g.sb * elem_size) % 16 == 0 &&
-                                 (g.ss * elem_size) % 16 == 0 && (g.sh * elem_size) % 16 == 0 &&
-                                 (g.v_off < 0 || (g.v_off * elem_size) % 16 == 0);
-                if (vec)
-                    DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
-                                 k_new, v_new, T, n_chunks, sel_idx, kmax, c0, l0);
-                else
-                    DARIC_LAUNCH((merge_kernel<1>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
-                                 k_new, v_new, T, n_chunks, sel_idx, kmax, c0, l0);
-            }
+            const dim3 grid(static_cast<unsigned>((kmax + kMergeTok - 1) / kMergeTok), static_cast<unsigned>(nc),
+                            static_cast<unsigned>(nl));
+            const bool vec = (g.D * elem_size) % 16 == 0 && (g.sb * elem_size) % 16 == 0 &&
+                             (g.ss * elem_size) % 16 == 0 && (g.sh * elem_size) % 16 == 0 &&
+                             (g.v_off < 0 || (g.v_off * elem_size) % 16 == 0);
+            if (vec)
+                DARIC_LAUNCH((merge_kernel<16>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
+                             k_new, v_new, T, n_chunks, sel_idx, kmax, c0, l0);
+            else
+                DARIC_LAUNCH((merge_kernel<1>), grid, kThreads, 0, stream, d, layer_off, g, elem_size, block_table,
+                             k_new, v_new, T, n_chunks, sel_idx, kmax, c0, l0);
             check_launch("merge_rows");
         }
     }
@@ -686,9 +697,10 @@ constexpr size_t kSelectMergeMaxLds = 48 * 1024;
 // A fused workgroup merges its chunk's selected rows alone, in rounds of
 // kMergeThreads x kMergeUnits 16-byte units. Up to this many rounds per chunk
 // the fused top-k + merge beat topk_kernel + merge_rows_kernel on MI355X
-// (config 3: 77 rows of 4 KiB, 10 rounds, 0.74-0.76 ms against 0.79 ms);
-// beyond it the merge kernel's spread over (chunk, row batch) wins (config 5:
-// 205 quantised rows, 26 rounds, 0.39 ms against 0.36 ms).
+// (config 3: 77 rows of 4 KiB, 10 rounds, 0.635 ms against 0.039 + 0.611 ms,
+// both layer-minor); beyond it the merge kernel's spread over (chunk, row
+// batch) wins (config 5: 205 quantised rows, 26 rounds, 0.39 ms against
+// 0.36 ms).
 constexpr int64_t kFusedMaxRounds = 12;
 
 bool select_merge_fits(const KVGeom& g, int elem_size, bool quant, int64_t max_tokens, int64_t kmax,
@@ -719,36 +731,31 @@ void launch_select_merge(const DescArg& d, int layer_off, int n_layers, const KV
     // deviation scales: per-head K scales of an fp8 cache (the quantising
     // merge's K scales are the same ones)
     const float* dev_scales = cache_kind == kE4M3 ? k_scales : nullptr;
-    for (int l0 = 0; l0 < n_layers; l0 += kMaxGridYZ) {
-        const int nl = std::min(kMaxGridYZ, n_layers - l0);
-        // grid.x holds the chunks; more than 2^31 - 1 is refused by the caller
-        for (int c0 = 0; c0 < n_chunks; c0 += kMaxGridYZ) {
-            const int nc = std::min(kMaxGridYZ, n_chunks - c0);
-            const dim3 grid(static_cast<unsigned>(nc), static_cast<unsigned>(nl));
-#define DARIC_SM(C, N, M, DN, WK) DARIC_LAUNCH((select_merge_kernel<C, N, M, DN, WK>), grid, kThreads, lds, stream, \
+    // one workgroup per (layer, chunk), layer-minor
+    for_layer_minor(n_layers, n_chunks, [&](const LayerMinor& lm, unsigned blocks) {
+#define DARIC_SM(C, N, M, DN, WK) DARIC_LAUNCH((select_merge_kernel<C, N, M, DN, WK>), blocks, kThreads, lds, stream, \
                                            d, layer_off, g, elem_size, block_table, k_new, v_new, T, n_chunks, \
                                            dev_scales, keys, sel_idx, kmax, n_max, units, dtu, dupr, \
-                                           k_scales, v_scales, c0, l0)
+                                           k_scales, v_scales, lm)
 #define DARIC_SM_K(C, N, M, DN) do { if (with_keys) DARIC_SM(C, N, M, DN, true); else DARIC_SM(C, N, M, DN, false); } while (0)
 #define DARIC_SM_D(C, N, M) do { if (dense) DARIC_SM_K(C, N, M, true); else DARIC_SM_K(C, N, M, false); } while (0)
-            if (cache_kind == kBF16) {
-                if (new_kind == kBF16) DARIC_SM_D(kBF16, kBF16, kMergeCopy);
-                else DARIC_SM_D(kBF16, kF16, kMergeCopy);
-            } else if (cache_kind == kF16) {
-                if (new_kind == kBF16) DARIC_SM_D(kF16, kBF16, kMergeCopy);
-                else DARIC_SM_D(kF16, kF16, kMergeCopy);
-            } else if (quant) {
-                if (new_kind == kBF16) DARIC_SM_D(kE4M3, kBF16, kMergeFromBF16);
-                else DARIC_SM_D(kE4M3, kF16, kMergeFromF16);
-            } else {
-                throw Error(DARIC_ERR_INVALID, "select_merge on an fp8 cache merges bf16/fp16 rows with scales");
-            }
+        if (cache_kind == kBF16) {
+            if (new_kind == kBF16) DARIC_SM_D(kBF16, kBF16, kMergeCopy);
+            else DARIC_SM_D(kBF16, kF16, kMergeCopy);
+        } else if (cache_kind == kF16) {
+            if (new_kind == kBF16) DARIC_SM_D(kF16, kBF16, kMergeCopy);
+            else DARIC_SM_D(kF16, kF16, kMergeCopy);
+        } else if (quant) {
+            if (new_kind == kBF16) DARIC_SM_D(kE4M3, kBF16, kMergeFromBF16);
+            else DARIC_SM_D(kE4M3, kF16, kMergeFromF16);
+        } else {
+            throw Error(DARIC_ERR_INVALID, "select_merge on an fp8 cache merges bf16/fp16 rows with scales");
+        }
 #undef DARIC_SM_D
 #undef DARIC_SM_K
 #undef DARIC_SM
-            check_launch("select_merge");
-        }
-    }
+        check_launch("select_merge");
+    });
 }
 
 }  // namespace daric
