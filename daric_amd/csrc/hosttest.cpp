@@ -2,6 +2,7 @@
 // the fast divider that the kernels use, compiled for the host from the same
 // headers. Not part of the product ABI (include/daric_cache_ops.h).
 #include <cstdint>
+#include <vector>
 
 #include "elem.h"
 #include "kernels.h"
@@ -37,6 +38,35 @@ int64_t daric_hosttest_fastdiv_errors(uint32_t d, uint32_t n0, uint32_t n1) {
     for (uint64_t n = n0; n < n1; ++n)
         if (f.div(static_cast<uint32_t>(n)) != static_cast<uint32_t>(n) / d) ++bad;
     return bad;
+}
+
+
+// Walks the launches for_layer_minor makes for n_layers x n_items and
+// decodes every block with LayerMinor::at_block. Returns the number of
+// launches when every (layer, item) pair is covered exactly once and no
+// launch exceeds kMaxGridBlocks, else -1 (a pair missed, repeated or out of
+// range) or -2 (an oversized launch).
+int64_t daric_hosttest_layer_minor(int n_layers, int64_t n_items) {
+    std::vector<uint8_t> seen(static_cast<size_t>(n_layers) * static_cast<size_t>(n_items), 0);
+    int64_t launches = 0;
+    bool bad = false, big = false;
+    daric::for_layer_minor(n_layers, n_items, [&](const daric::LayerMinor& lm, unsigned blocks) {
+        ++launches;
+        if (static_cast<int64_t>(blocks) > daric::kMaxGridBlocks || blocks == 0) big = true;
+        for (uint32_t b = 0; b < blocks; ++b) {
+            int l;
+            int64_t w;
+            lm.at_block(b, l, w);
+            if (l < 0 || l >= n_layers || w < 0 || w >= n_items) { bad = true; continue; }
+            uint8_t& s = seen[static_cast<size_t>(l) * static_cast<size_t>(n_items) + static_cast<size_t>(w)];
+            if (s) bad = true;
+            s = 1;
+        }
+    });
+    for (uint8_t s : seen)
+        if (!s) bad = true;
+    if (big) return -2;
+    return bad ? -1 : launches;
 }
 
 }

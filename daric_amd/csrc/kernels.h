@@ -50,13 +50,17 @@ struct LayerMinor {
     int32_t l0 = 0;     // first layer of the launch
     int32_t nl = 1;     // layers of the launch
     int64_t w0 = 0;     // first work item of the launch
+    // (layer, work item) of block b of the launch
 #ifdef __HIPCC__
-    __device__ inline void at(int& l, int64_t& w) const {
-        const uint32_t b = blockIdx.x;
+    __host__ __device__
+#endif
+    inline void at_block(uint32_t b, int& l, int64_t& w) const {
         const uint32_t n = static_cast<uint32_t>(nl);
         l = l0 + static_cast<int>(b % n);
         w = w0 + static_cast<int64_t>(b / n);
     }
+#ifdef __HIPCC__
+    __device__ inline void at(int& l, int64_t& w) const { at_block(blockIdx.x, l, w); }
 #endif
 };
 

@@ -186,9 +186,9 @@ __global__ __launch_bounds__(kThreads) void rerotate_lane_kernel(
     const DescPtr<RopeSeg> segs = desc_at<RopeSeg>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
     int lyr;
-    int64_t w;
-    lm.at(lyr, w);
-    const int tile = static_cast<int>(w);
+    int64_t item;
+    lm.at(lyr, item);
+    const int tile = static_cast<int>(item);
     const RopeSeg sg = desc_load(segs + find_segment(segs, n_segs, tile));
     if (sg.delta == 0.0f) return;
     const int page = sg.tok_start / g.PS + ((tile - sg.tile_begin) >> log2_parts);

@@ -496,10 +496,10 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
     // work item w = (chunk, row batch), batches of a chunk consecutive
     int l;
-    int64_t w;
-    lm.at(l, w);
-    const int ci = static_cast<int>(w / nbx);
-    const int bx = static_cast<int>(w - static_cast<int64_t>(ci) * nbx);
+    int64_t item;
+    lm.at(l, item);
+    const int ci = static_cast<int>(item / nbx);
+    const int bx = static_cast<int>(item - static_cast<int64_t>(ci) * nbx);
     const SelChunk c = desc_load(chunks + ci);
     const int tid = static_cast<int>(threadIdx.x);
     const int ses = MODE == kMergeCopy ? ces : 2;                    // source element size
@@ -540,9 +540,9 @@ __global__ __launch_bounds__(kThreads) void select_merge_kernel(
     const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
     int l;
-    int64_t w;
-    lm.at(l, w);
-    const int ci = static_cast<int>(w);
+    int64_t item;
+    lm.at(l, item);
+    const int ci = static_cast<int>(item);
     const SelChunk c = desc_load(chunks + ci);
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & 63;

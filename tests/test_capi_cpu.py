@@ -47,6 +47,8 @@ def hosttest(lib):
     h.daric_hosttest_fastdiv_errors.restype = ctypes.c_int64
     h.daric_hosttest_quant_quotients.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                                  ctypes.c_int64, ctypes.c_void_p]
+    h.daric_hosttest_layer_minor.argtypes = [ctypes.c_int, ctypes.c_int64]
+    h.daric_hosttest_layer_minor.restype = ctypes.c_int64
     return h
 
 
@@ -493,3 +495,19 @@ def test_select_merge_validation(lib):
     assert "smaller than a chunk's k" in run(bf, sel_t=small)[1]
     past = (_lib.DaricChunk * 1)(_lib.DaricChunk(6, 0, 40, 4, 5))   # tokens 5..44 from page 6: page 8
     assert "reads past the end of block_table" in run(bf, chunk=past)[1]
+
+
+# (layers, items, launches): the merge at configs 3 and 5 (items = row batches x
+# chunks), the in-place kernel at config 2 (page parts), one layer and one
+# item, and grids past 2^24 - 1 blocks cut into launches by items or by layers.
+@pytest.mark.parametrize("n_layers,n_items,launches", [
+    (32, 1920, 1), (80, 416, 1), (32, 896, 1), (1, 1, 1), (3, 7, 1), (7, 5, 1),
+    (80, 300_000, 2), (2, (1 << 24) - 1, 3), (1, 1 << 24, 2), ((1 << 24) + 5, 2, 4),
+])
+def test_layer_minor_grid_covers_every_pair_once(hosttest, n_layers, n_items, launches):
+    """The layer-minor block order of the merge, the fused top-k + merge and
+    the in-place lane kernel: every (layer, work item) pair is taken by
+    exactly one block of exactly one launch, no launch passes 2^24 - 1 blocks
+    (grid.x x 256 lanes < 2^32), and the grid is cut only when it must be."""
+    assert hosttest.daric_hosttest_layer_minor(n_layers, n_items) == launches
+
