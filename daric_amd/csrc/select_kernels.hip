@@ -494,7 +494,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(
     __shared__ int64_t s_dst[kMergeMaxTok];   // byte offset of the token's K row in the layer
     const DescPtr<SelChunk> chunks = desc_at<SelChunk>(d, 0);
     const DescPtr<uint8_t*> layers = desc_at<uint8_t*>(d, layer_off);
-    // work item w = (chunk, row batch), batches of a chunk consecutive
+    // work item = (chunk, row batch), the batches of a chunk consecutive
     int l;
     int64_t item;
     lm.at(l, item);
