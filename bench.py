@@ -417,6 +417,72 @@ def run_placement(steps, warmup, seed=0):
     return out
 
 
+LAYOUTS = (  # (blocks per layer, layer stride in bytes)
+    (8192, 512 << 20),
+    (8192, 4 << 30),
+    (32768, 2 << 30),
+    (32768, 4 << 30),
+    (65536, 4 << 30),
+)
+
+
+def run_layout(steps, warmup, seed=0):
+    """The headline's 256 jobs (same staging, 512 seeded random pages per
+    layer) on 32 layer caches carved from one 132 GiB allocation at the
+    layer strides of LAYOUTS, fused call and plain scatter timed alternately,
+    three rounds each (kernel-time medians): how the layers' spacing in memory
+    sets the rate. Opt-in (--extra layout)."""
+    from daric_amd import cache_ops
+    dev = torch.device("cuda:0")
+    cfg = CFG2
+    H, D, PS = cfg["kv_heads"], cfg["head_dim"], cfg["block_size"]
+    span = PS * H * D * 2
+    w = build_workload(cfg, dev, num_blocks=1024, seed=seed)
+    del w["cache"]
+    torch.cuda.empty_cache()
+    L, C, CT = w["L"], cfg["chunks"], cfg["chunk_tokens"]
+    pages_per_chunk = CT // PS
+    need = max((L - 1) * stride + 2 * nb * span for nb, stride in LAYOUTS)
+    big = torch.empty(need, dtype=torch.uint8, device=dev)
+    j = w["jobs"]
+    inv = w["inv_freq"].to(dev)
+    stream = torch.cuda.current_stream(dev)
+    g = torch.Generator().manual_seed(seed)
+    runs = []
+    for nb, stride in LAYOUTS:
+        cp = cache_ops.CacheCopier()
+        for l, name in enumerate(w["names"]):
+            o = l * stride
+            cp.register_layer(name, big[o:o + 2 * nb * span].view(torch.bfloat16).view(2, nb, PS, H, D), False)
+        cp.register_store(w["staging"])
+        pages = (torch.randperm(nb - 1, generator=g)[: C * pages_per_chunk] + 1).tolist()
+        # job order as build_workload's: chunk-major, then the layers
+        flat = [p for c in range(C) for _ in range(L) for p in pages[c * pages_per_chunk:(c + 1) * pages_per_chunk]]
+        idx = torch.tensor(flat, dtype=torch.int32, device=dev)
+        fused = (lambda cp=cp, idx=idx: cp.scatter_pages_rerotate(
+            j["names"], j["offsets"], j["sizes"], idx, j["ioff"], j["deltas"], j["ntok"], inv, D, True,
+            stream.cuda_stream))
+        plain = (lambda cp=cp, idx=idx: cp.scatter_pages(j["names"], j["offsets"], j["sizes"], idx, j["ioff"],
+                                                          stream.cuda_stream))
+        runs.append((nb, stride, fused, plain))
+    times = {(nb, stride): ([], []) for nb, stride, _, _ in runs}
+    for _ in range(3):
+        for nb, stride, fused, plain in runs:
+            times[(nb, stride)][0].append(time_steps(fused, steps, warmup, stream)["kern_ms"])
+            times[(nb, stride)][1].append(time_steps(plain, steps, warmup, stream)["kern_ms"])
+    nbytes = algorithmic_bytes(cfg)
+    out = []
+    for nb, stride in LAYOUTS:
+        f, p = (float(np.median(x)) for x in times[(nb, stride)])
+        out.append(dict(blocks_per_layer=nb, layer_stride_GiB=stride / (1 << 30), fused_kernel_ms=f,
+                        fused_GBps=_gbps(nbytes, f), plain_kernel_ms=p, plain_GBps=_gbps(nbytes, p)))
+    del big, runs
+    torch.cuda.empty_cache()
+    return dict(layouts=out, note="headline jobs on 32 layer caches carved from one allocation at the "
+                                  "given layer stride (same staging, seeded random pages); fused call "
+                                  "and plain scatter alternating, median of 3 rounds")
+
+
 def run_config2_hnd(steps, warmup, seed=0):
     """Config 2's return path on a head-major cache: the request's 8 x 1024
     tokens in 32 layers of a [2, 65536, 16, 8, 128] bf16 cache stored HND
@@ -929,7 +995,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--extra", default="2h,3,4,5",
                     help="other BASELINE configs to measure after the headline (comma list of 2h, 3, 4, "
-                         "5, or 'none'; 'place' adds the cache-placement check, 258 GiB)")
+                         "5, or 'none'; 'place' adds the cache-placement check, 258 GiB; 'layout' the "
+                         "layer-stride check, 129 GiB)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (torch copy_) `steps` times, the "
                          "known-size reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -950,9 +1017,9 @@ def main():
     torch.cuda.empty_cache()
     extra = {}
     runners = {"2h": run_config2_hnd, "3": run_config3, "4": run_config4, "5": run_config5,
-               "place": run_placement}
+               "place": run_placement, "layout": run_layout}
     for cname in [x.strip() for x in a.extra.split(",") if x.strip() and x.strip() != "none"]:
-        key = "placement" if cname == "place" else f"config{cname}"
+        key = {"place": "placement", "layout": "layer_layout"}.get(cname, f"config{cname}")
         # a secondary configuration that raises (out of memory on a shared
         # box, say) is recorded as such; the headline line is still printed
         try:
